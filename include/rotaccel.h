@@ -1,0 +1,146 @@
+/*
+ * rotaccel.h -- C ABI of librotaccel.so, the MI355X (gfx950) W8A16 INT8 GEMM
+ * library behind the rotalabs_accel Python API.
+ *
+ * Conventions
+ *  - Every pointer is a device pointer (HBM) unless stated otherwise. The
+ *    library never allocates, frees or retains device memory: callers own
+ *    inputs, outputs and streams.
+ *  - Matrices are row-major with an explicit leading dimension in ELEMENTS.
+ *    Weights are int8 [N, K] (nn.Linear layout: one row per output channel),
+ *    scales fp32 [N] (one per output channel).
+ *  - `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ *    Every entry point only enqueues work; none synchronises the host.
+ *  - Every entry point returns RA_OK (0) or an ra_status code; the C side
+ *    never aborts or throws. ra_strerror() turns a code into text.
+ *  - dtype codes: RA_F16, RA_BF16, RA_F32 (see enum ra_dtype).
+ */
+#ifndef ROTACCEL_H
+#define ROTACCEL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RA_ABI_VERSION 1
+
+enum ra_dtype { RA_F16 = 0, RA_BF16 = 1, RA_F32 = 2 };
+
+enum ra_status {
+  RA_OK = 0,
+  RA_ERR_ARG = 1,       /* bad size / leading dimension / null pointer       */
+  RA_ERR_DTYPE = 2,     /* unsupported dtype combination                      */
+  RA_ERR_LAUNCH = 3,    /* kernel launch failed (hipGetLastError != success)  */
+  RA_ERR_VARIANT = 4,   /* a forced kernel variant cannot run this shape      */
+  RA_ERR_DEVICE = 5     /* no usable device / not a gfx950 device             */
+};
+
+/* Kernel variants for ra_w8a16_gemm_ex. RA_VARIANT_AUTO picks by shape. */
+enum ra_variant {
+  RA_VARIANT_AUTO = 0,
+  RA_VARIANT_SKINNY = 1,  /* split-K MFMA skinny GEMM (decode, small M)        */
+  RA_VARIANT_TILED = 2,   /* LDS-staged double-buffered MFMA GEMM (prefill)   */
+  RA_VARIANT_GENERIC = 3, /* any shape / alignment / dtype, VALU, slow        */
+  RA_VARIANT_GEMV = 4     /* decode GEMV, M <= 4, x staged in LDS             */
+};
+
+/* Version of this ABI (RA_ABI_VERSION of the built library). */
+int ra_abi_version(void);
+
+/* Static text for an ra_status code. Never NULL. */
+const char *ra_strerror(int code);
+
+/*
+ * y[M,N] = x[M,K] @ (w[N,K] * scale[N,None]).T (+ bias[N])
+ *
+ * Replaces the reference's GPU branch of int8_gemm:
+ *   src/rotalabs_accel/kernels/gemm.py:234-235 (dispatch) ->
+ *   _int8_gemm_triton gemm.py:140-186 -> _int8_gemm_kernel gemm.py:53-138.
+ * Same arithmetic as the kernel there: exact int8 -> fp16/bf16 conversion,
+ * fp32 accumulation, per-output-channel scale applied to the fp32 accumulator
+ * (gemm.py:133); bias is added to the fp32 value before the single rounding to
+ * the output dtype (the reference adds it after rounding, gemm.py:181-182).
+ * Differences by design: w is read in its [N,K] layout (no per-call
+ * transpose, gemm.py:157-160), and y has the activation dtype (the reference
+ * fallback's output dtype, gemm.py:46) instead of always fp16 (gemm.py:162).
+ *
+ * x_dtype: RA_F16 | RA_BF16 | RA_F32 (y has the same dtype).
+ * bias: NULL or [N] of bias_dtype (RA_F16 | RA_BF16 | RA_F32).
+ * ldx >= K, ldw >= K, ldy >= N. M, N, K >= 0 (M == 0 or N == 0: no-op;
+ * K == 0: y = bias or 0).
+ */
+int ra_w8a16_gemm(const void *x, int64_t ldx, int x_dtype,
+                  const int8_t *w, int64_t ldw, const float *scale,
+                  const void *bias, int bias_dtype,
+                  void *y, int64_t ldy,
+                  int64_t M, int64_t N, int64_t K, void *stream);
+
+/* ra_w8a16_gemm with an explicit kernel variant (enum ra_variant); used by
+ * tests to run every kernel on the same inputs. Returns RA_ERR_VARIANT if the
+ * forced variant cannot handle the shape, dtype or alignment. */
+int ra_w8a16_gemm_ex(const void *x, int64_t ldx, int x_dtype,
+                     const int8_t *w, int64_t ldw, const float *scale,
+                     const void *bias, int bias_dtype,
+                     void *y, int64_t ldy,
+                     int64_t M, int64_t N, int64_t K, int variant, void *stream);
+
+/* Which variant RA_VARIANT_AUTO runs for this problem (enum ra_variant). */
+int ra_w8a16_gemm_select(int64_t M, int64_t N, int64_t K, int x_dtype);
+
+/*
+ * Fused gate/up projection with SwiGLU epilogue:
+ *   g = x @ (w[0:I]  * s[0:I]).T,   u = x @ (w[I:2I] * s[I:2I]).T
+ *   h[M,I] = silu(g) * u            (fp32 math, one rounding to x_dtype)
+ * w is the row-concatenation [Wg; Wu] of two per-channel-quantized [I,K]
+ * weights (per-row quantization makes this identical to quantizing [2I,K]).
+ * Replaces int8_gemm (gemm.py:189-238) twice followed by swiglu_fused
+ * (src/rotalabs_accel/kernels/activations.py:108-138, kernel :51-80).
+ * x_dtype: RA_F16 | RA_BF16. ldh >= I.
+ */
+int ra_w8a16_gateup_swiglu(const void *x, int64_t ldx, int x_dtype,
+                           const int8_t *w, int64_t ldw, const float *scale,
+                           void *h, int64_t ldh,
+                           int64_t M, int64_t I, int64_t K, void *stream);
+
+/*
+ * y[r,:] = (x[r,:] * rsqrt(mean(x[r,:]^2) + eps)) rounded to x_dtype, times
+ * weight, rounded to y_dtype -- the two roundings of rmsnorm_torch
+ * (src/rotalabs_accel/kernels/normalization.py:32-45); math in fp32.
+ * Replaces the GPU branch of rmsnorm (normalization.py:208-213 ->
+ * _rmsnorm_triton :141-160 -> _rmsnorm_kernel :67-101).
+ * x_dtype, w_dtype, y_dtype: RA_F16 | RA_BF16 | RA_F32; y_dtype must be the
+ * promotion of x_dtype and w_dtype (as torch promotes x.to(x.dtype) * w).
+ */
+int ra_rmsnorm(const void *x, int64_t ldx, int x_dtype,
+               const void *weight, int w_dtype,
+               void *y, int64_t ldy, int y_dtype,
+               int64_t rows, int64_t hidden, float eps, void *stream);
+
+/*
+ * out[i] = silu(gate[i]) * up[i] over n contiguous elements, fp32 math, one
+ * rounding. Replaces swiglu_fused's GPU branch
+ * (src/rotalabs_accel/kernels/activations.py:131-135 -> _swiglu_kernel :51-80).
+ */
+int ra_swiglu(const void *gate, const void *up, void *out, int64_t n,
+              int dtype, void *stream);
+
+/*
+ * Per-output-channel symmetric int8 quantization of w[N,K] (w_dtype RA_F32,
+ * RA_F16 or RA_BF16), bit-exact with quantize_weight_per_channel on the CPU
+ * (src/rotalabs_accel/quantization/symmetric.py:126-151 ->
+ * quantize_symmetric(dim=1) :24-82): s = max|w_row| / 127 with IEEE division
+ * (rounded to w_dtype for fp16/bf16), s = 1 for all-zero rows,
+ * q = clamp(round_half_even(w / s), -128, 127); scale written as fp32.
+ */
+int ra_quantize_per_channel(const void *w, int64_t ldw, int w_dtype,
+                            int64_t N, int64_t K,
+                            int8_t *q, int64_t ldq, float *scale, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ROTACCEL_H */

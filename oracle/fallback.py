@@ -1,0 +1,78 @@
+"""torch-CPU restatement of the reference's PyTorch fallback for the W8A16 path.
+
+The reference's own fallback *is* a sequence of torch ops, so the restatement
+uses the same ops, on CPU tensors only:
+
+  int8_gemm_torch  src/rotalabs_accel/kernels/gemm.py:31-48
+                   = F.linear(x, dequantize(W, s, dtype=x.dtype, dim=0), bias)
+  dequantize       src/rotalabs_accel/quantization/symmetric.py:85-123
+                   = (q.float() * s[:, None]).to(dtype)
+  rmsnorm_torch    src/rotalabs_accel/kernels/normalization.py:32-45
+                   = (x.float() * rsqrt(mean(x.float()^2, -1) + eps)).to(x.dtype) * w
+  swiglu_torch     src/rotalabs_accel/kernels/activations.py:36-45
+                   = silu(gate) * up
+
+plus ``mlp_ref`` (RMSNorm -> gate/up -> SwiGLU -> down, the decoder-MLP
+composition of the reference's SwiGLU module, activations.py:141-178, with
+int8 projections) and float64 numpy references used for tolerance budgets.
+
+This is also the CPU baseline that ``bench.py`` times ("port" kind).
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+
+def dequantize_ref(q: torch.Tensor, s: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    return (q.float() * s.unsqueeze(1)).to(dtype)
+
+
+def int8_gemm_ref(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor, bias=None) -> torch.Tensor:
+    """gemm.py:31-48 on CPU tensors."""
+    assert not x.is_cuda and not q.is_cuda and not s.is_cuda
+    return F.linear(x, dequantize_ref(q, s, x.dtype), bias)
+
+
+def rmsnorm_ref(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """normalization.py:32-45 on CPU tensors."""
+    xf = x.float()
+    r = torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return (xf * r).to(x.dtype) * w
+
+
+def swiglu_ref(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """activations.py:36-45 on CPU tensors."""
+    return F.silu(gate) * up
+
+
+def mlp_ref(x, norm_w, q_gu, s_gu, q_down, s_down, eps: float = 1e-6):
+    """RMSNorm -> Int8 gate+up (one [2I,H] weight) -> SwiGLU -> Int8 down."""
+    inter = q_gu.shape[0] // 2
+    h = rmsnorm_ref(x, norm_w, eps)
+    gu = int8_gemm_ref(h, q_gu, s_gu)
+    a = swiglu_ref(gu[..., :inter], gu[..., inter:])
+    return int8_gemm_ref(a, q_down, s_down)
+
+
+# ---------------------------------------------------------- float64 references
+def gemm_f64(x: np.ndarray, q: np.ndarray, s: np.ndarray, bias=None) -> np.ndarray:
+    """y = x @ (fp32(q*s)).T (+ bias), accumulated in float64.
+
+    The dequantized weight is the single fp32 product ``q*s`` (no rounding to
+    the activation dtype); this is the 'fp32-accumulated reference' against
+    which both the fallback and the kernels are within tolerance.
+    """
+    w = (q.astype(np.float32) * s.astype(np.float32)[:, None]).astype(np.float64)
+    y = x.astype(np.float64) @ w.T
+    if bias is not None:
+        y = y + bias.astype(np.float64)
+    return y
+
+
+def swiglu_f64(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    g = g.astype(np.float64)
+    return g / (1.0 + np.exp(-g)) * u.astype(np.float64)

@@ -1,0 +1,118 @@
+"""numpy restatement of the reference's symmetric int8 quantization.
+
+Follows src/rotalabs_accel/quantization/symmetric.py:
+  quantize_symmetric           :24-82
+  dequantize                   :85-123
+  quantize_weight_per_channel  :126-151
+  calculate_quantization_error :154-207
+
+Reduced-precision inputs (fp16, bf16) follow PyTorch's CPU semantics for the
+same op sequence: every elementwise op is computed in fp32 and rounded once to
+the tensor dtype (round-to-nearest-even). bf16 is carried as uint16 bit
+patterns because numpy has no bf16 type.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+QMAX = 127  # symmetric.py:57
+
+
+# ---------------------------------------------------------------- bf16 helpers
+def f32_to_bf16_bits(a: np.ndarray) -> np.ndarray:
+    """Round fp32 to bf16 (round-to-nearest-even), return uint16 bit patterns."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    nan = np.isnan(a)
+    out = rounded.astype(np.uint16)
+    out[nan] = 0x7FC0
+    return out
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def round_to(a32: np.ndarray, dtype: str) -> np.ndarray:
+    """Round an fp32 array to ``dtype`` and return the rounded values as fp32."""
+    if dtype == "f32":
+        return a32.astype(np.float32)
+    if dtype == "f16":
+        return a32.astype(np.float16).astype(np.float32)
+    if dtype == "bf16":
+        return bf16_bits_to_f32(f32_to_bf16_bits(a32))
+    raise ValueError(dtype)
+
+
+# ------------------------------------------------------------- quantization
+def quantize_symmetric(t32: np.ndarray, dtype: str = "f32", dim: int | None = None):
+    """Closed form of quantize_symmetric (symmetric.py:24-82).
+
+    ``t32`` holds the tensor's values as fp32 (they must already be
+    representable in ``dtype``). Returns (q int8, scale fp32).
+
+    Steps, each rounded to ``dtype`` as the CPU tensor ops do:
+      max_val = |t|.amax(dim, keepdim)           (:62 / :66, exact)
+      scale   = round(max_val / 127)            (:63 / :67, true division)
+      scale   = 1 where scale == 0              (:70)
+      q       = int8(clamp(rne(round(t / scale)), -128, 127))   (:73)
+      scale   = scale.float(); squeeze(dim)     (:76-80)
+    """
+    t32 = np.asarray(t32, dtype=np.float32)
+    a = np.abs(t32)
+    if dim is None:
+        max_val = a.max() if a.size else np.float32(0)
+        max_val = np.asarray(max_val, dtype=np.float32)
+    else:
+        max_val = a.max(axis=dim, keepdims=True)
+    scale = round_to(np.asarray(max_val / np.float32(QMAX), dtype=np.float32), dtype)
+    scale = np.where(scale == 0, np.float32(1.0), scale).astype(np.float32)
+    ratio = round_to((t32 / scale).astype(np.float32), dtype)
+    q = np.clip(np.rint(ratio), -128, 127).astype(np.int8)
+    scale = scale.astype(np.float32)
+    if dim is not None:
+        scale = np.squeeze(scale, axis=dim)
+    return q, scale
+
+
+def quantize_weight_per_channel(w32: np.ndarray, dtype: str = "f32"):
+    """symmetric.py:126-151: 2-D only, one scale per output row (reduce dim=1)."""
+    w32 = np.asarray(w32, dtype=np.float32)
+    assert w32.ndim == 2, f"Expected 2D weight matrix, got {w32.ndim}D"
+    return quantize_symmetric(w32, dtype, dim=1)
+
+
+def dequantize(q: np.ndarray, scale: np.ndarray, dtype: str = "f16", dim: int | None = None):
+    """symmetric.py:85-123: fp32(q) * scale (one fp32 product), rounded to dtype.
+
+    Returns fp32 values that are exactly representable in ``dtype``.
+    """
+    qf = q.astype(np.float32)
+    s = np.asarray(scale, dtype=np.float32)
+    if s.ndim == 1 and q.ndim == 2:
+        s = s[:, None] if dim in (None, 0) else s[None, :]
+    return round_to((qf * s).astype(np.float32), dtype)
+
+
+def calculate_quantization_error(orig32: np.ndarray, q: np.ndarray, scale: np.ndarray,
+                                 dtype: str = "f32", dim: int | None = None) -> dict:
+    """symmetric.py:154-207, with sums done in float64 (so values agree with the
+    reference to float32 reduction-order noise, not bit-for-bit)."""
+    restored = dequantize(q, scale, dtype, dim)
+    diff = round_to((orig32 - restored).astype(np.float32), dtype).astype(np.float64)
+    o = orig32.astype(np.float64)
+    thr = np.abs(o).max() * 0.1
+    mask = np.abs(o) > thr
+    rel = float((np.abs(diff[mask]) / np.abs(o[mask])).max() * 100) if mask.any() else 0.0
+    signal = (o ** 2).mean()
+    noise = (diff ** 2).mean()
+    return {
+        "max_abs_error": float(np.abs(diff).max()),
+        "mean_abs_error": float(np.abs(diff).mean()),
+        "relative_error_pct": rel,
+        "snr_db": float(10 * np.log10(signal / (noise + 1e-10))),
+    }

@@ -1,0 +1,157 @@
+// C ABI of librotaccel.so (declared in include/rotaccel.h): argument checks,
+// kernel selection and error mapping. No device memory is allocated here.
+#include "ra_internal.h"
+
+namespace {
+
+using namespace ra;
+
+bool valid_act(int dt) { return dt == RA_F16 || dt == RA_BF16 || dt == RA_F32; }
+
+int to_status(hipError_t e) { return e == hipSuccess ? RA_OK : RA_ERR_LAUNCH; }
+
+#ifdef RA_TUNING
+// Tuning builds only (-DRA_TUNING): force the skinny configuration.
+SkinnyCfg g_skinny_override{0, 0, 0};
+#endif
+
+SkinnyCfg skinny_config(int64_t M, int64_t N, int64_t K) {
+  SkinnyCfg c = skinny_select(M, N, K);
+#ifdef RA_TUNING
+  if (g_skinny_override.mt) c = g_skinny_override;
+#endif
+  return c;
+}
+
+// M above which the tiled kernel is used (below it the weight stream dominates
+// and the skinny split-K kernel is faster).
+constexpr int64_t kSkinnyMaxM = 64;
+
+int select_variant(const GemmArgs &a) {
+  if (a.K == 0) return RA_VARIANT_GENERIC;
+  if (gemv_supported(a)) return RA_VARIANT_GEMV;
+  if (a.M <= kSkinnyMaxM && skinny_supported(a)) return RA_VARIANT_SKINNY;
+  if (tiled_supported(a)) return RA_VARIANT_TILED;
+  if (skinny_supported(a)) return RA_VARIANT_SKINNY;
+  return RA_VARIANT_GENERIC;
+}
+
+int check_gemm(const GemmArgs &a) {
+  if (a.M < 0 || a.N < 0 || a.K < 0) return RA_ERR_ARG;
+  if (a.M > INT32_MAX || a.N > INT32_MAX || a.K > INT32_MAX) return RA_ERR_ARG;
+  if (!valid_act(a.x_dt)) return RA_ERR_DTYPE;
+  if (a.bias && !valid_act(a.bias_dt)) return RA_ERR_DTYPE;
+  if (a.M == 0 || a.N == 0) return RA_OK;
+  if (!a.y || !a.scale || !a.w || (a.K > 0 && !a.x)) return RA_ERR_ARG;
+  if (a.ldx < a.K || a.ldw < a.K || a.ldy < a.N) return RA_ERR_ARG;
+  return RA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+#ifdef RA_TUNING
+void ra_tune_skinny(int mt, int rt, int nw) { g_skinny_override = SkinnyCfg{mt, rt, nw}; }
+#endif
+
+int ra_abi_version(void) { return RA_ABI_VERSION; }
+
+const char *ra_strerror(int code) {
+  switch (code) {
+    case RA_OK: return "success";
+    case RA_ERR_ARG: return "rotaccel: invalid argument (size, leading dimension or null pointer)";
+    case RA_ERR_DTYPE: return "rotaccel: unsupported dtype";
+    case RA_ERR_LAUNCH: return "rotaccel: kernel launch failed";
+    case RA_ERR_VARIANT: return "rotaccel: the requested kernel variant cannot run this problem";
+    case RA_ERR_DEVICE: return "rotaccel: no usable gfx950 device";
+    default: return "rotaccel: unknown error";
+  }
+}
+
+int ra_w8a16_gemm_ex(const void *x, int64_t ldx, int x_dtype, const int8_t *w, int64_t ldw,
+                     const float *scale, const void *bias, int bias_dtype, void *y, int64_t ldy, int64_t M,
+                     int64_t N, int64_t K, int variant, void *stream) {
+  const GemmArgs a{x, ldx, x_dtype, w, ldw, scale, bias, bias_dtype, y, ldy, M, N, K};
+  int st = check_gemm(a);
+  if (st != RA_OK) return st;
+  if (M == 0 || N == 0) return RA_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int v = variant == RA_VARIANT_AUTO ? select_variant(a) : variant;
+  switch (v) {
+    case RA_VARIANT_SKINNY:
+      if (!skinny_supported(a) || K == 0) return RA_ERR_VARIANT;
+      return to_status(skinny_launch(a, skinny_config(M, N, K), s));
+    case RA_VARIANT_GEMV:
+      if (!gemv_supported(a)) return RA_ERR_VARIANT;
+      return to_status(gemv_launch(a, s));
+    case RA_VARIANT_TILED:
+      if (!tiled_supported(a) || K == 0) return RA_ERR_VARIANT;
+      return to_status(tiled_launch(a, s));
+    case RA_VARIANT_GENERIC:
+      return to_status(generic_launch(a, s));
+    default:
+      return RA_ERR_ARG;
+  }
+}
+
+int ra_w8a16_gemm(const void *x, int64_t ldx, int x_dtype, const int8_t *w, int64_t ldw, const float *scale,
+                  const void *bias, int bias_dtype, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                  void *stream) {
+  return ra_w8a16_gemm_ex(x, ldx, x_dtype, w, ldw, scale, bias, bias_dtype, y, ldy, M, N, K, RA_VARIANT_AUTO,
+                          stream);
+}
+
+int ra_w8a16_gemm_select(int64_t M, int64_t N, int64_t K, int x_dtype) {
+  // Alignment is assumed satisfied (contiguous, 16-byte aligned operands).
+  const GemmArgs a{reinterpret_cast<const void *>(256), K, x_dtype, reinterpret_cast<const int8_t *>(256),
+                   K, nullptr, nullptr, RA_F32, nullptr, N, M, N, K};
+  return select_variant(a);
+}
+
+int ra_w8a16_gateup_swiglu(const void *x, int64_t ldx, int x_dtype, const int8_t *w, int64_t ldw,
+                           const float *scale, void *h, int64_t ldh, int64_t M, int64_t I, int64_t K,
+                           void *stream) {
+  if (M < 0 || I < 0 || K < 0 || M > INT32_MAX || 2 * I > INT32_MAX || K > INT32_MAX) return RA_ERR_ARG;
+  if (x_dtype != RA_F16 && x_dtype != RA_BF16 && x_dtype != RA_F32) return RA_ERR_DTYPE;
+  if (M == 0 || I == 0) return RA_OK;
+  if (!h || !w || !scale || (K > 0 && !x)) return RA_ERR_ARG;
+  if (ldx < K || ldw < K || ldh < I) return RA_ERR_ARG;
+  const GateUpArgs a{x, ldx, x_dtype, w, ldw, scale, h, ldh, M, I, K};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (K > 0 && gateup_gemv_supported(a)) return to_status(gateup_gemv_launch(a, s));
+  if (K > 0 && M <= kSkinnyMaxM && gateup_skinny_supported(a)) return to_status(gateup_skinny_launch(a, s));
+  if (K > 0 && gateup_tiled_supported(a)) return to_status(gateup_tiled_launch(a, s));
+  return to_status(gateup_generic_launch(a, s));
+}
+
+int ra_rmsnorm(const void *x, int64_t ldx, int x_dtype, const void *weight, int w_dtype, void *y, int64_t ldy,
+               int y_dtype, int64_t rows, int64_t hidden, float eps, void *stream) {
+  if (rows < 0 || hidden < 0 || rows > INT32_MAX || hidden > INT32_MAX) return RA_ERR_ARG;
+  if (!valid_act(x_dtype) || !valid_act(w_dtype) || !valid_act(y_dtype)) return RA_ERR_DTYPE;
+  const int promoted = x_dtype == w_dtype ? x_dtype : RA_F32;
+  if (y_dtype != promoted) return RA_ERR_DTYPE;
+  if (rows == 0 || hidden == 0) return RA_OK;
+  if (!x || !weight || !y || ldx < hidden || ldy < hidden) return RA_ERR_ARG;
+  return to_status(rmsnorm_launch(x, ldx, x_dtype, weight, w_dtype, y, ldy, y_dtype, rows, hidden, eps,
+                                  static_cast<hipStream_t>(stream)));
+}
+
+int ra_swiglu(const void *gate, const void *up, void *out, int64_t n, int dtype, void *stream) {
+  if (n < 0) return RA_ERR_ARG;
+  if (!valid_act(dtype)) return RA_ERR_DTYPE;
+  if (n == 0) return RA_OK;
+  if (!gate || !up || !out) return RA_ERR_ARG;
+  return to_status(swiglu_launch(gate, up, out, n, dtype, static_cast<hipStream_t>(stream)));
+}
+
+int ra_quantize_per_channel(const void *w, int64_t ldw, int w_dtype, int64_t N, int64_t K, int8_t *q,
+                            int64_t ldq, float *scale, void *stream) {
+  if (N < 0 || K < 0 || N > INT32_MAX || K > INT32_MAX) return RA_ERR_ARG;
+  if (!valid_act(w_dtype)) return RA_ERR_DTYPE;
+  if (N == 0) return RA_OK;
+  if (!w || !q || !scale || ldw < K || ldq < K) return RA_ERR_ARG;
+  return to_status(quantize_launch(w, ldw, w_dtype, N, K, q, ldq, scale, static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

@@ -1,0 +1,173 @@
+// Shared device helpers for the gfx950 W8A16 kernels: vector types, exact
+// int8 -> fp16/bf16 dequantisation, MFMA wrappers and dtype conversions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rotaccel.h"
+
+namespace ra {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <typename To, typename From>
+__device__ __forceinline__ To bitcast(const From &v) {
+  static_assert(sizeof(To) == sizeof(From), "bitcast size mismatch");
+  return __builtin_bit_cast(To, v);
+}
+
+// ---------------------------------------------------------------------------
+// int8 -> fp16, exact. Magic-number conversion (Kim et al. 2022, "Who Says
+// Elephants Can't Run: Bringing Large Scale MoE Models into Cloud Scale
+// Production", also used by FasterTransformer): the fp16 whose bit pattern is
+// 0x64UU equals 1024 + UU; with UU = q ^ 0x80 = q + 128 it equals 1152 + q, so
+// one packed subtraction of 1152 (exact in fp16) yields q for two lanes.
+// Cost: 1 xor per 4 values, 1 v_perm + 1 v_pk_add_f16 per 2 values.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t dq2_f16(uint32_t t, uint32_t sel) {
+  const f16x2 magic = {(_Float16)1152.0f, (_Float16)1152.0f};
+  const uint32_t biased = __builtin_amdgcn_perm(0x64646464u, t, sel);
+  return bitcast<uint32_t>(bitcast<f16x2>(biased) - magic);
+}
+
+// 8 int8 (w0 = bytes 0..3, w1 = bytes 4..7) -> 8 fp16 in element order.
+__device__ __forceinline__ uint4 dq8_f16(uint32_t w0, uint32_t w1) {
+  const uint32_t t0 = w0 ^ 0x80808080u, t1 = w1 ^ 0x80808080u;
+  uint4 r;
+  r.x = dq2_f16(t0, 0x04010400u);  // bytes 0,1
+  r.y = dq2_f16(t0, 0x04030402u);  // bytes 2,3
+  r.z = dq2_f16(t1, 0x04010400u);
+  r.w = dq2_f16(t1, 0x04030402u);
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// int8 -> bf16, exact. A signed byte converts to fp32 in one instruction
+// (v_cvt_f32_i32 with an SDWA sign-extended byte select); |q| <= 128 needs at
+// most 8 significant bits, so the fp32 value's upper half IS the bf16 value
+// and packing two upper halves (one v_perm) is exact. 1.5 VALU ops per value.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pack_hi16(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+__device__ __forceinline__ uint4 dq8_bf16(uint32_t w0, uint32_t w1) {
+  uint4 r;
+  r.x = pack_hi16((float)(int8_t)(w0), (float)(int8_t)(w0 >> 8));
+  r.y = pack_hi16((float)(int8_t)(w0 >> 16), (float)(int8_t)(w0 >> 24));
+  r.z = pack_hi16((float)(int8_t)(w1), (float)(int8_t)(w1 >> 8));
+  r.w = pack_hi16((float)(int8_t)(w1 >> 16), (float)(int8_t)(w1 >> 24));
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// Scalar conversions between fp32 and the 16-bit storage types (RNE).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float f16_to_f32(uint16_t b) { return (float)bitcast<_Float16>(b); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ uint16_t f32_to_f16(float v) { return bitcast<uint16_t>((_Float16)v); }
+__device__ __forceinline__ uint16_t f32_to_bf16(float v) { return bitcast<uint16_t>((__bf16)v); }
+
+__device__ __forceinline__ float load_as_f32(const void *p, int64_t i, int dt) {
+  if (dt == RA_F32) return static_cast<const float *>(p)[i];
+  const uint16_t b = static_cast<const uint16_t *>(p)[i];
+  return dt == RA_F16 ? f16_to_f32(b) : bf16_to_f32(b);
+}
+
+__device__ __forceinline__ void store_from_f32(void *p, int64_t i, int dt, float v) {
+  if (dt == RA_F32) {
+    static_cast<float *>(p)[i] = v;
+  } else {
+    static_cast<uint16_t *>(p)[i] = dt == RA_F16 ? f32_to_f16(v) : f32_to_bf16(v);
+  }
+}
+
+// Round an fp32 value to fp16 / bf16 and back (the rounding torch applies when
+// an fp32 intermediate is stored in a reduced-precision tensor).
+__device__ __forceinline__ float round_through(float v, int dt) {
+  if (dt == RA_F16) return (float)(_Float16)v;
+  if (dt == RA_BF16) return (float)(__bf16)v;
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Activation-type traits: dequantiser, MFMA instructions, output conversion.
+// MFMA operand layouts (gfx950, wave64):
+//  16x16x32: A[i][k] from lane i + 16*(k/8), element k%8;
+//            B[k][j] from lane j + 16*(k/8), element k%8;
+//            D[i][j] in lane j + 16*(i/4), element i%4.
+//  32x32x16: A[i][k] from lane i + 32*(k/8), element k%8;
+//            B[k][j] from lane j + 32*(k/8), element k%8;
+//            D[i][j] in lane j + 32*((i/4)%2), element (i%4) + 4*(i/8).
+// Only the row / column mappings matter to the kernels: the sum over k is the
+// same for any permutation of k applied identically to A and B.
+// ---------------------------------------------------------------------------
+template <int DT>
+struct Act;
+
+template <>
+struct Act<RA_F16> {
+  static __device__ __forceinline__ uint4 dq8(uint32_t w0, uint32_t w1) { return dq8_f16(w0, w1); }
+  static __device__ __forceinline__ f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<f16x8>(a), bitcast<f16x8>(b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(bitcast<f16x8>(a), bitcast<f16x8>(b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t out(float v) { return f32_to_f16(v); }
+  static __device__ __forceinline__ float in(uint16_t b) { return f16_to_f32(b); }
+  static __device__ __forceinline__ float rnd(float v) { return (float)(_Float16)v; }
+};
+
+template <>
+struct Act<RA_BF16> {
+  static __device__ __forceinline__ uint4 dq8(uint32_t w0, uint32_t w1) { return dq8_bf16(w0, w1); }
+  static __device__ __forceinline__ f32x4 mfma16(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(bitcast<bf16x8>(a), bitcast<bf16x8>(b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(bitcast<bf16x8>(a), bitcast<bf16x8>(b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t out(float v) { return f32_to_bf16(v); }
+  static __device__ __forceinline__ float in(uint16_t b) { return bf16_to_f32(b); }
+  static __device__ __forceinline__ float rnd(float v) { return (float)(__bf16)v; }
+};
+
+// Wave64 sum (all lanes receive the total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// SwiGLU of a gate/up pair with the roundings of the reference composition
+// int8_gemm (gate, up stored in the activation dtype) -> swiglu_torch
+// (F.silu and the product each computed in fp32 and stored in that dtype),
+// src/rotalabs_accel/kernels/gemm.py:46 and kernels/activations.py:45.
+template <typename A>
+__device__ __forceinline__ uint16_t swiglu_out(float g32, float u32) {
+  const float g = A::rnd(g32), u = A::rnd(u32);
+  const float sg = A::rnd(g / (1.0f + expf(-g)));
+  return A::out(sg * u);
+}
+
+// Epilogue value: fp32 accumulator * per-channel scale (+ bias), in fp32.
+__device__ __forceinline__ float epilogue_value(float acc, const float *scale, const void *bias,
+                                                int bias_dt, int n) {
+  float v = acc * scale[n];
+  if (bias) v += load_as_f32(bias, n, bias_dt);
+  return v;
+}
+
+}  // namespace ra

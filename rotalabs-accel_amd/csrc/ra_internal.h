@@ -1,0 +1,72 @@
+// Host-side declarations shared by the kernel translation units and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rotaccel.h"
+
+namespace ra {
+
+struct GemmArgs {
+  const void *x;
+  int64_t ldx;
+  int x_dt;
+  const int8_t *w;
+  int64_t ldw;
+  const float *scale;
+  const void *bias;  // may be null
+  int bias_dt;
+  void *y;
+  int64_t ldy;
+  int64_t M, N, K;
+};
+
+// Skinny (split-K MFMA) kernel: MT 16-wide activation tiles, RT 16-row weight
+// tiles per workgroup, NW waves splitting K.
+struct SkinnyCfg {
+  int mt, rt, nw;
+};
+bool skinny_supported(const GemmArgs &a);
+SkinnyCfg skinny_select(int64_t M, int64_t N, int64_t K);
+hipError_t skinny_launch(const GemmArgs &a, const SkinnyCfg &c, hipStream_t s);
+
+// Tiled (LDS-staged MFMA) kernel for large M.
+bool tiled_supported(const GemmArgs &a);
+hipError_t tiled_launch(const GemmArgs &a, hipStream_t s);
+
+// Generic kernel: any shape, alignment and activation dtype.
+hipError_t generic_launch(const GemmArgs &a, hipStream_t s);
+
+// Fused gate/up + SwiGLU.
+struct GateUpArgs {
+  const void *x;
+  int64_t ldx;
+  int x_dt;
+  const int8_t *w;
+  int64_t ldw;
+  const float *scale;
+  void *h;
+  int64_t ldh;
+  int64_t M, I, K;
+};
+bool gateup_skinny_supported(const GateUpArgs &a);
+hipError_t gateup_skinny_launch(const GateUpArgs &a, hipStream_t s);
+bool gateup_tiled_supported(const GateUpArgs &a);
+hipError_t gateup_tiled_launch(const GateUpArgs &a, hipStream_t s);
+hipError_t gateup_generic_launch(const GateUpArgs &a, hipStream_t s);
+
+// Decode GEMV (M <= 4, x staged in LDS, one HBM round trip per wave).
+bool gemv_supported(const GemmArgs &a);
+hipError_t gemv_launch(const GemmArgs &a, hipStream_t s);
+bool gateup_gemv_supported(const GateUpArgs &a);
+hipError_t gateup_gemv_launch(const GateUpArgs &a, hipStream_t s);
+
+hipError_t rmsnorm_launch(const void *x, int64_t ldx, int x_dt, const void *w, int w_dt, void *y,
+                          int64_t ldy, int y_dt, int64_t rows, int64_t hidden, float eps,
+                          hipStream_t s);
+hipError_t swiglu_launch(const void *g, const void *u, void *o, int64_t n, int dt, hipStream_t s);
+hipError_t quantize_launch(const void *w, int64_t ldw, int w_dt, int64_t N, int64_t K, int8_t *q,
+                           int64_t ldq, float *scale, hipStream_t s);
+
+}  // namespace ra

@@ -1,0 +1,29 @@
+"""W8A16 path kernels (re-export names as src/rotalabs_accel/kernels/__init__.py:38-42).
+
+HAS_TRITON is kept for import compatibility and is always False: the GPU
+kernels here are hand-written HIP for gfx950 (see HAS_HIP).
+"""
+from rotalabs_accel._backend import available as _hip_available
+from rotalabs_accel.kernels.activations import swiglu_fused, swiglu_torch
+from rotalabs_accel.kernels.gemm import Int8Linear, int8_gemm, int8_gemm_torch
+from rotalabs_accel.kernels.mlp import Int8SwiGLUMLP, int8_gateup_swiglu, int8_mlp
+from rotalabs_accel.kernels.normalization import TritonRMSNorm, rmsnorm, rmsnorm_torch
+
+HAS_TRITON = False
+HAS_HIP = _hip_available()
+
+__all__ = [
+    "HAS_TRITON",
+    "HAS_HIP",
+    "rmsnorm",
+    "rmsnorm_torch",
+    "TritonRMSNorm",
+    "swiglu_fused",
+    "swiglu_torch",
+    "int8_gemm",
+    "int8_gemm_torch",
+    "Int8Linear",
+    "int8_gateup_swiglu",
+    "int8_mlp",
+    "Int8SwiGLUMLP",
+]

@@ -1,0 +1,72 @@
+"""The C ABI library loads and exports every symbol include/rotaccel.h
+declares; host-side argument checks return the documented codes without any
+device work (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from rotalabs_accel import _backend
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "rotaccel.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ra_\w+)\s*\(", src, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _backend.load()
+    names = _declared()
+    assert "ra_w8a16_gemm" in names and len(names) >= 8
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_abi_version_matches_header():
+    ver = int(re.search(r"#define RA_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
+    assert _backend.load().ra_abi_version() == ver == _backend.ABI_VERSION
+
+
+def test_strerror_all_codes():
+    lib = _backend.load()
+    for code in range(0, 7):
+        assert lib.ra_strerror(code)
+
+
+def test_argument_checks_without_device_work():
+    lib = _backend.load()
+    n = None
+    # negative / oversized sizes
+    assert lib.ra_w8a16_gemm(n, 0, 0, n, 0, n, n, 0, n, 0, -1, 4, 4, n) == 1
+    # unsupported activation dtype
+    assert lib.ra_w8a16_gemm(n, 0, 7, n, 0, n, n, 0, n, 0, 1, 4, 4, n) == 2
+    # empty problems are no-ops
+    assert lib.ra_w8a16_gemm(n, 0, 0, n, 0, n, n, 0, n, 0, 0, 4, 4, n) == 0
+    assert lib.ra_w8a16_gemm(n, 0, 0, n, 0, n, n, 0, n, 0, 4, 0, 4, n) == 0
+    # null pointers / leading dimensions
+    assert lib.ra_w8a16_gemm(n, 4, 0, n, 4, n, n, 0, n, 4, 2, 4, 4, n) == 1
+    assert lib.ra_rmsnorm(n, 0, 1, n, 1, n, 0, 0, 1, 8, 1e-6, n) == 2   # y dtype != promotion
+    assert lib.ra_swiglu(n, n, n, -1, 0, n) == 1
+    assert lib.ra_quantize_per_channel(n, 0, 9, 1, 1, n, 0, n, n) == 2
+    assert lib.ra_w8a16_gateup_swiglu(n, 0, 0, n, 0, n, n, 0, 0, 8, 8, n) == 0
+    # unknown forced variant
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.addressof(buf)
+    assert lib.ra_w8a16_gemm_ex(p, 16, 0, p, 16, p, n, 0, p, 16, 1, 16, 16, 99, n) == 1
+
+
+@pytest.mark.parametrize("M,expect", [(1, 4), (4, 4), (5, 1), (16, 1), (64, 1), (65, 2), (2048, 2)])
+def test_variant_selection(M, expect):
+    assert _backend.load().ra_w8a16_gemm_select(M, 11008, 4096, 0) == expect
+
+
+def test_variant_selection_fallbacks():
+    lib = _backend.load()
+    assert lib.ra_w8a16_gemm_select(1, 8192, 28672, 1) == 1  # K beyond one GEMV workgroup -> skinny
+    assert lib.ra_w8a16_gemm_select(1, 64, 50, 0) == 3     # K % 16 != 0 -> generic
+    assert lib.ra_w8a16_gemm_select(1, 64, 64, 2) == 3     # fp32 activations -> generic
+    assert lib.ra_w8a16_gemm_select(4, 64, 0, 0) == 3      # K == 0 -> generic (bias / zeros)

@@ -1,0 +1,209 @@
+"""The product's Python API on CPU tensors: same names, results and errors as
+the reference (its own tests, tests/test_imports.py:116-233, plus bit-level
+checks against the oracle and the golden vectors)."""
+import hashlib
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import rotalabs_accel as ra
+from oracle import fallback
+from oracle import quant as oq
+from workloads import PLUMBING_SHAPE, gemm_case
+
+
+def _t16(bits, dt):
+    return torch.from_numpy(bits.astype(np.int16)).view(dt)
+
+
+# ---- the reference's own unit tests, on this package -----------------------
+def test_int8_gemm_torch_shape():
+    x = torch.randn(2, 8, 64)
+    w = torch.randint(-128, 127, (128, 64), dtype=torch.int8)
+    out = ra.int8_gemm_torch(x, w, torch.ones(128))
+    assert out.shape == (2, 8, 128) and not torch.isnan(out).any()
+
+
+def test_quantize_dequantize_roundtrip():
+    x = torch.randn(64, 128)
+    q, s = ra.quantize_symmetric(x)
+    assert q.dtype == torch.int8
+    r = ra.dequantize(q, s)
+    assert r.shape == x.shape and (x - r).abs().mean() < 0.1
+
+
+def test_per_channel_shapes():
+    w = torch.randn(64, 128)
+    q, s = ra.quantize_weight_per_channel(w)
+    assert q.dtype == torch.int8 and q.shape == w.shape and s.shape == (64,)
+
+
+def test_quantization_error_keys():
+    x = torch.randn(64, 128)
+    q, s = ra.quantize_symmetric(x)
+    e = ra.calculate_quantization_error(x, q, s)
+    assert set(e) == {"max_abs_error", "mean_abs_error", "relative_error_pct", "snr_db"}
+    assert e["max_abs_error"] >= 0
+
+
+@pytest.mark.parametrize("cls", [ra.Int8Linear, ra.QuantizedLinear])
+def test_linear_modules(cls):
+    lin = cls(in_features=64, out_features=128)
+    lin.quantize_weights(torch.randn(128, 64))
+    out = lin(torch.randn(2, 8, 64))
+    assert out.shape == (2, 8, 128) and not torch.isnan(out).any()
+
+
+def test_rmsnorm_module():
+    norm = ra.TritonRMSNorm(hidden_size=64, eps=1e-6)
+    x = torch.randn(2, 8, 64)
+    assert norm(x).shape == x.shape
+
+
+# ---- bit-level agreement with the oracle / golden vectors --------------------
+def test_quantize_fp32_bit_exact():
+    g = torch.Generator().manual_seed(11)
+    w = torch.randn(96, 257, generator=g) * 0.02
+    w[0] = 0
+    w[1, :9] = torch.tensor([127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -125.5])
+    w[1, 9:] = 0
+    q, s = ra.quantize_weight_per_channel(w)
+    q_o, s_o = oq.quantize_weight_per_channel(w.numpy())
+    assert np.array_equal(q.numpy(), q_o) and np.array_equal(s.numpy(), s_o)
+
+
+@pytest.mark.parametrize("name,dt", [("f16", torch.float16), ("bf16", torch.bfloat16)])
+def test_quantize_reduced_bit_exact(golden, name, dt):
+    w = _t16(golden[f"qpc_{name}_w"], dt)
+    q, s = ra.quantize_weight_per_channel(w)
+    assert np.array_equal(q.numpy(), golden[f"qpc_{name}_q"])
+    assert np.array_equal(s.numpy(), golden[f"qpc_{name}_s"])
+
+
+@pytest.mark.parametrize("name,dt", [("f16", torch.float16), ("bf16", torch.bfloat16), ("f32", torch.float32)])
+def test_int8_gemm_cpu_golden(golden, name, dt):
+    x = torch.from_numpy(golden["gemm_x_f32"]).to(dt)
+    q = torch.from_numpy(golden["gemm_q"])
+    s = torch.from_numpy(golden["gemm_s"])
+    b = torch.from_numpy(golden["gemm_b_f32"]).to(dt)
+    y, yb = ra.int8_gemm(x, q, s), ra.int8_gemm(x, q, s, b)
+    if dt == torch.float32:
+        assert np.array_equal(y.numpy(), golden["gemm_y_f32"]) and np.array_equal(yb.numpy(), golden["gemm_yb_f32"])
+    else:
+        assert torch.equal(y, _t16(golden[f"gemm_y_{name}"], dt))
+        assert torch.equal(yb, _t16(golden[f"gemm_yb_{name}"], dt))
+
+
+def test_plumbing_workload_digest(golden_digests):
+    """int8_gemm on CPU at x fp16 [16,4096], W [4096,4096], seed 0 reproduces
+    the reference's output bit for bit (sha256)."""
+    M, K, N, seed = PLUMBING_SHAPE
+    c = gemm_case(M, K, N, seed)
+
+    def sha(t):
+        a = t.contiguous()
+        if a.dtype in (torch.float16, torch.bfloat16):
+            a = a.view(torch.int16)
+        return hashlib.sha256(a.numpy().tobytes()).hexdigest()
+
+    assert sha(c.x) == golden_digests["x_f16"]
+    assert sha(c.q) == golden_digests["q"] and sha(c.s) == golden_digests["s"]
+    y = ra.int8_gemm(c.x, c.q, c.s)
+    assert y.dtype == torch.float16 and y.shape == (16, 4096)
+    assert sha(y) == golden_digests["y_f16"]
+
+
+def test_gateup_and_mlp_cpu_match_oracle():
+    g = torch.Generator().manual_seed(3)
+    H, inter, M = 64, 96, 5
+    x = torch.randn(M, H, generator=g).bfloat16()
+    nw = (1 + 0.01 * torch.randn(H, generator=g)).bfloat16()
+    wg, wu, wd = (torch.randn(inter, H, generator=g) * 0.02, torch.randn(inter, H, generator=g) * 0.02,
+                  torch.randn(H, inter, generator=g) * 0.02)
+    mlp = ra.Int8SwiGLUMLP(H, inter, norm_dtype=torch.bfloat16)
+    mlp.quantize_weights(wg, wu, wd)
+    mlp.norm_weight.data.copy_(nw)
+    y = mlp(x)
+    ref = fallback.mlp_ref(x, nw, mlp.weight_gate_up, mlp.scale_gate_up, mlp.weight_down, mlp.scale_down)
+    assert torch.equal(y, ref)
+    # concatenated quantization == separate quantization (row independence)
+    q_all, s_all = ra.quantize_weight_per_channel(torch.cat([wg, wu]))
+    assert torch.equal(q_all, mlp.weight_gate_up) and torch.equal(s_all, mlp.scale_gate_up)
+
+
+# ---- error behaviour ---------------------------------------------------------
+def test_int8_gemm_asserts():
+    x = torch.randn(4, 64)
+    with pytest.raises(AssertionError, match="Weight must be INT8"):
+        ra.int8_gemm(x, torch.zeros(8, 64), torch.ones(8))
+    with pytest.raises(AssertionError, match="Weight shape mismatch"):
+        ra.int8_gemm(x, torch.zeros(8, 32, dtype=torch.int8), torch.ones(8))
+    with pytest.raises(AssertionError, match="Scale shape mismatch"):
+        ra.int8_gemm(x, torch.zeros(8, 64, dtype=torch.int8), torch.ones(7))
+
+
+def test_bias_dtype_mismatch_raises_on_cpu():
+    x = torch.randn(2, 64).half()
+    w = torch.zeros(8, 64, dtype=torch.int8)
+    with pytest.raises(RuntimeError):
+        ra.int8_gemm(x, w, torch.ones(8), torch.zeros(8))
+
+
+@pytest.mark.parametrize("cls", [ra.Int8Linear, ra.QuantizedLinear])
+def test_unquantized_forward_raises(cls):
+    with pytest.raises(RuntimeError, match="Weights not quantized"):
+        cls(16, 8)(torch.randn(2, 16))
+
+
+def test_state_dict_keys_and_reload():
+    lin = ra.Int8Linear(32, 16, bias=True)
+    lin.quantize_weights(torch.randn(16, 32))
+    sd = lin.state_dict()
+    assert set(sd) == {"weight_int8", "scale", "weight_transposed", "bias"}
+    assert sd["bias"].dtype == torch.float16 and sd["weight_transposed"].shape == (32, 16)
+    assert torch.equal(sd["weight_transposed"], sd["weight_int8"].t())
+    fresh = ra.Int8Linear(32, 16, bias=True)
+    fresh.load_state_dict(sd)
+    with pytest.raises(RuntimeError):          # _quantized is not part of the state
+        fresh(torch.randn(2, 32))
+    ql = ra.QuantizedLinear(32, 16, bias=True)
+    assert set(ql.state_dict()) == {"weight_int8", "weight_scale", "bias"}
+
+
+def test_from_linear():
+    lin = torch.nn.Linear(32, 16, bias=True)
+    a = ra.Int8Linear.from_linear(lin)
+    q, s = ra.quantize_weight_per_channel(lin.weight.data)
+    assert torch.equal(a.weight_int8, q) and torch.equal(a.scale, s) and a.bias.dtype == torch.float16
+    b = ra.QuantizedLinear.from_linear(lin)
+    assert torch.equal(b.weight_int8, q) and b.bias.dtype == torch.float32
+
+
+def test_rows_helper_layouts():
+    from rotalabs_accel.kernels.gemm import _rows
+    t = torch.randn(6, 40).half()
+    v, ld = _rows(t, 16)
+    assert v.data_ptr() == t.data_ptr() and ld == 40
+    sl = torch.randn(6, 48).half()[:, :40]           # row stride 48 (96 B: 16-aligned)
+    v, ld = _rows(sl, 16)
+    assert v.data_ptr() == sl.data_ptr() and ld == 48
+    tt = torch.randn(40, 6).half().t()               # column-major -> copy
+    v, ld = _rows(tt, 16)
+    assert ld == 40 and v.is_contiguous() and torch.equal(v, tt)
+    odd = torch.randn(1, 40).half().expand(3, 40)    # row stride 0 -> copy
+    v, ld = _rows(odd, 16)
+    assert ld == 40 and torch.equal(v, odd)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    code = ("import sys; sys.path.insert(0, %r)\n"
+            "from rotalabs_accel import _backend\n"
+            "try:\n    _backend.load()\nexcept RuntimeError as e:\n    print('RAISED', e)\n") % (
+        os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "rotalabs-accel_amd"))
+    env = dict(os.environ, ROTACCEL_LIB=str(tmp_path / "nope.so"))
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
+    assert "RAISED" in out.stdout and "Build it" in out.stdout

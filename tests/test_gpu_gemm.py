@@ -1,0 +1,264 @@
+"""GPU parity of the W8A16 GEMM kernels (through the C ABI).
+
+* Exact known answers: integer activations and weights with small sums, so
+  every partial sum and the rounded output are exact and any indexing
+  mistake shows up as a mismatch -- for every kernel variant.
+* Tolerance vs the oracle (the reference fallback restated on the CPU,
+  rtol = atol = 1e-2) and vs a float64 reference (tighter, per dtype).
+* Full-size workloads vs an fp32 torch reference on the GPU, plus rows
+  re-checked against the float64 oracle on the CPU.
+* Determinism, bias dtypes, strides / misalignment, K tails, graph replay.
+"""
+import numpy as np
+import pytest
+import torch
+
+import rotalabs_accel as ra
+from oracle import fallback
+from rotalabs_accel import _backend
+from rotalabs_accel.kernels.gemm import _int8_gemm_hip
+from workloads import DECODE_SHAPES, PREFILL_SHAPES, SMALLBATCH_SHAPES, gemm_case
+
+pytestmark = pytest.mark.gpu
+
+SKINNY, TILED, GENERIC, GEMV = (_backend.VARIANT_SKINNY, _backend.VARIANT_TILED, _backend.VARIANT_GENERIC,
+                                _backend.VARIANT_GEMV)
+ALL_VARIANTS = (GEMV, SKINNY, TILED, GENERIC)
+
+# fp64 tolerance per output dtype: ~2 ulp relative + accumulation noise
+TOL64 = {torch.float16: (2e-3, 2e-3), torch.bfloat16: (8e-3, 8e-3), torch.float32: (1e-5, 1e-4)}
+
+
+def _run(x, q, s, bias=None, variant=_backend.VARIANT_AUTO):
+    """One GEMM through the C ABI; None if a forced variant reports that it
+    cannot run this shape (RA_ERR_VARIANT)."""
+    print(f"  gemm M={x.reshape(-1, x.shape[-1]).shape[0]} K={x.shape[-1]} N={q.shape[0]} "
+          f"dt={x.dtype} variant={variant}", flush=True)
+    try:
+        y = _int8_gemm_hip(x, q, s, bias, variant)
+    except RuntimeError as e:
+        if variant != _backend.VARIANT_AUTO and "variant cannot run" in str(e):
+            return None
+        raise
+    torch.cuda.synchronize()
+    return y
+
+
+def _exact_case(M, K, N, dt, seed, dev, bias=False):
+    """Integer x in {-1,0,1}, q in [-lim, lim], scale 2^-4 (exact), optional
+    integer bias * 2^-4: |sum| stays small enough to be exact in dt."""
+    g = torch.Generator().manual_seed(seed)
+    lim = 3 if dt == torch.float16 else 1
+    x = torch.randint(-1, 2, (M, K), generator=g).float()
+    if dt == torch.bfloat16:   # keep |sum| <= 255: at most 127 nonzeros per row
+        keep = torch.rand(M, K, generator=g) < min(1.0, 127.0 / K)
+        x = x * keep
+    q = torch.randint(-lim, lim + 1, (N, K), generator=g).to(torch.int8)
+    s = torch.full((N,), 2.0 ** -4)
+    b = (torch.randint(-8, 9, (N,), generator=g).float() * 2.0 ** -4) if bias else None
+    exact = (x.double() @ q.double().T) * 2.0 ** -4
+    if b is not None:
+        exact = exact + b.double()
+    return (x.to(dt).to(dev), q.to(dev), s.to(dev), None if b is None else b.to(dt).to(dev), exact)
+
+
+EXACT_SHAPES = [
+    (1, 64, 16), (1, 48, 43), (2, 4096, 64), (1, 11008, 40), (3, 128, 77), (16, 1040, 33),
+    (17, 64, 130), (33, 96, 50), (64, 256, 96), (65, 256, 300), (256, 128, 128), (300, 320, 200),
+    (513, 1024, 129), (1000, 64, 17),
+]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K,N", EXACT_SHAPES)
+def test_exact_known_answer_all_variants(gpu, M, K, N, dt):
+    x, q, s, b, exact = _exact_case(M, K, N, dt, seed=M * 7 + K + N, dev=gpu, bias=(M % 2 == 1))
+    want = exact.to(dt)
+    ran = 0
+    for v in ALL_VARIANTS:
+        y = _run(x, q, s, b, v)
+        if y is None:
+            assert v == GEMV and (M > 4 or K > 16384), f"variant {v} refused M={M} K={K}"
+            continue
+        y = y.cpu()
+        ran += 1
+        assert y.dtype == dt
+        assert torch.equal(y, want), f"variant {v}: {(y.double() - exact).abs().max()}"
+    assert ran >= 3
+
+
+def test_exact_fp32_activations(gpu):
+    x, q, s, b, exact = _exact_case(9, 200, 70, torch.float32, seed=5, dev=gpu, bias=True)
+    y = _run(x, q, s, b).cpu()
+    assert y.dtype == torch.float32 and torch.equal(y.double(), exact)
+
+
+UNIT_ROUNDOFF = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8, torch.float32: 2.0 ** -24}
+
+
+def _oracle_check(y, x_cpu, q_cpu, s_cpu, b_cpu=None):
+    """Parity of a kernel output y (CPU tensor) on CPU-sized problems.
+
+    1. Against the fp32-accumulated dequantize-then-matmul reference (float64
+       here; weights = the fp32 products q*s that dequantize forms before its
+       final cast): rtol = atol = 1e-2, and a tighter per-dtype bound.
+    2. Against the reference fallback's exact bits (oracle): the same
+       rtol = atol = 1e-2 plus the fallback's own provable error from rounding
+       the dequantized weights to x.dtype, u * (|x| @ |w|^T).
+    """
+    xn = x_cpu.float().numpy()
+    y64 = fallback.gemm_f64(xn, q_cpu.numpy(), s_cpu.numpy(), None if b_cpu is None else b_cpu.float().numpy())
+    yd = y.double().numpy()
+    err = np.abs(yd - y64)
+    assert (err <= 1e-2 + 1e-2 * np.abs(y64)).all(), f"max err {err.max()} vs fp32-accumulated reference"
+    rtol, atol = TOL64[y.dtype]
+    assert (err <= atol + rtol * np.abs(y64)).all(), f"max err {err.max()} above the {y.dtype} bound"
+    y_fb = fallback.int8_gemm_ref(x_cpu, q_cpu, s_cpu, b_cpu).double().numpy()
+    w_dt = fallback.dequantize_ref(q_cpu, s_cpu, x_cpu.dtype).double().numpy()
+    slack = UNIT_ROUNDOFF[x_cpu.dtype] * (np.abs(xn.astype(np.float64)) @ np.abs(w_dt).T)
+    err_fb = np.abs(yd - y_fb)
+    assert (err_fb <= 1e-2 + 1e-2 * np.abs(y_fb) + slack).all(), f"max err vs fallback {err_fb.max()}"
+
+
+TOL_SHAPES = [(1, 1024, 512), (4, 2048, 1024), (16, 4096, 1024), (17, 1024, 777), (64, 1024, 2048),
+              (100, 512, 384), (256, 1024, 1024), (512, 2048, 640)]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K,N", TOL_SHAPES)
+def test_random_vs_oracle(gpu, M, K, N, dt):
+    c = gemm_case(M, K, N, seed=M + K + N, dtype=dt, outlier_rows=True)
+    g = torch.Generator().manual_seed(99)
+    b = (torch.randn(N, generator=g) * 0.1).to(dt)
+    for v in (_backend.VARIANT_AUTO, GEMV, SKINNY, TILED):
+        y = _run(c.x.to(gpu), c.q.to(gpu), c.s.to(gpu), b.to(gpu), v)
+        if y is None:
+            assert v == GEMV and M > 4
+            continue
+        _oracle_check(y.cpu(), c.x, c.q, c.s, b)
+
+
+def _full_size_check(c, gpu):
+    """Full-size parity on the GPU: the reference is a float64 torch matmul
+    (at least as accurate as fp32 accumulation) of x and the fp32-dequantized
+    weight; the fallback's bits are bounded as in _oracle_check; a few rows
+    are re-checked against the float64 oracle on the CPU."""
+    x, q, s = c.x.to(gpu), c.q.to(gpu), c.s.to(gpu)
+    y = _run(x, q, s)
+    w32 = q.float() * s[:, None]
+    y32 = (x.double() @ w32.double().t().contiguous()).float()
+    err = (y.float() - y32).abs()
+    assert bool((err <= 1e-2 + 1e-2 * y32.abs()).all()), f"max err {err.max().item()}"
+    rtol, atol = TOL64[x.dtype]
+    assert bool((err <= atol + rtol * y32.abs()).all()), f"max err {err.max().item()} above the {x.dtype} bound"
+    w_dt = w32.to(x.dtype).float()
+    y_fb = (x.double() @ w_dt.double().t().contiguous()).float()   # fallback arithmetic, exact accumulation
+    slack = UNIT_ROUNDOFF[x.dtype] * (x.float().abs() @ w_dt.abs().t().contiguous())
+    err_fb = (y.float() - y_fb).abs()
+    assert bool((err_fb <= 1e-2 + 1e-2 * y_fb.abs() + slack).all())
+    del w32, w_dt
+    rows = sorted(set([0, c.M - 1, c.M // 2] + c.meta.get("outlier_rows", [])))[:8]
+    y64 = fallback.gemm_f64(c.x[rows].float().cpu().numpy(), c.q.cpu().numpy(), c.s.cpu().numpy())
+    np.testing.assert_allclose(y[rows].double().cpu().numpy(), y64, rtol=rtol, atol=atol)
+
+
+@pytest.mark.parametrize("M,K,N,seed", DECODE_SHAPES)
+def test_decode_full_size(gpu, M, K, N, seed):
+    _full_size_check(gemm_case(M, K, N, seed, device=gpu), gpu)
+
+
+@pytest.mark.parametrize("M,K,N,seed", SMALLBATCH_SHAPES)
+def test_smallbatch_full_size(gpu, M, K, N, seed):
+    _full_size_check(gemm_case(M, K, N, seed, device=gpu, outlier_rows=True), gpu)
+
+
+@pytest.mark.parametrize("M,K,N,seed", PREFILL_SHAPES)
+def test_prefill_full_size(gpu, M, K, N, seed):
+    _full_size_check(gemm_case(M, K, N, seed, device=gpu), gpu)
+
+
+@pytest.mark.parametrize("M", [1, 16, 2048])
+def test_deterministic(gpu, M):
+    c = gemm_case(M, 4096, 4096, seed=21, device=gpu)
+    a = _run(c.x, c.q, c.s)
+    b = _run(c.x, c.q, c.s)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("bdt", [torch.float16, torch.bfloat16, torch.float32])
+def test_bias_dtypes(gpu, bdt):
+    c = gemm_case(8, 512, 256, seed=3)
+    b = torch.randn(256) * 0.5
+    y = _run(c.x.to(gpu), c.q.to(gpu), c.s.to(gpu), b.to(bdt).to(gpu)).cpu()
+    ref = fallback.gemm_f64(c.x.float().numpy(), c.q.numpy(), c.s.numpy(), b.to(bdt).float().numpy())
+    np.testing.assert_allclose(y.double().numpy(), ref, rtol=2e-3, atol=2e-3)
+
+
+def test_strided_and_misaligned_inputs(gpu):
+    c = gemm_case(24, 512, 200, seed=8)
+    xb = torch.zeros(24, 520, dtype=torch.float16)
+    xb[:, 8:] = c.x
+    x_strided = xb.to(gpu)[:, 8:]                      # row stride 520, 16-B aligned start
+    y1 = ra.int8_gemm(x_strided, c.q.to(gpu), c.s.to(gpu)).cpu()
+    flat = torch.zeros(24 * 512 + 1, dtype=torch.float16)
+    flat[1:] = c.x.reshape(-1)
+    x_mis = flat.to(gpu)[1:].view(24, 512)            # 2-byte misaligned base
+    y2 = ra.int8_gemm(x_mis, c.q.to(gpu), c.s.to(gpu)).cpu()
+    x_t = c.x.t().contiguous().to(gpu).t()              # column-major
+    y3 = ra.int8_gemm(x_t, c.q.to(gpu), c.s.to(gpu)).cpu()
+    ref = ra.int8_gemm(c.x.to(gpu), c.q.to(gpu), c.s.to(gpu)).cpu()
+    assert torch.equal(y1, ref) and torch.equal(y2, ref) and torch.equal(y3, ref)
+    # odd K (not a multiple of 16) runs the generic kernel
+    c2 = gemm_case(5, 50, 37, seed=9)
+    y4 = ra.int8_gemm(c2.x.to(gpu), c2.q.to(gpu), c2.s.to(gpu)).cpu()
+    _oracle_check(y4, c2.x, c2.q, c2.s)
+
+
+def test_batched_leading_dims_and_modules(gpu):
+    g = torch.Generator().manual_seed(4)
+    lin = torch.nn.Linear(256, 320, bias=True)
+    m = ra.Int8Linear.from_linear(lin).to(gpu)
+    x = torch.randn(2, 7, 256, generator=g).half()
+    y = m(x.to(gpu)).cpu()
+    assert y.shape == (2, 7, 320) and y.dtype == torch.float16
+    ref = fallback.int8_gemm_ref(x.reshape(-1, 256), m.weight_int8.cpu(), m.scale.cpu(), m.bias.detach().cpu())
+    torch.testing.assert_close(y.reshape(-1, 320).float(), ref.float(), rtol=1e-2, atol=1e-2)
+    qm = ra.QuantizedLinear.from_linear(lin).to(gpu)
+    qm._quantized = True
+    yq = qm(x.to(gpu)).cpu()
+    torch.testing.assert_close(yq.float(), y.float(), rtol=2e-3, atol=2e-3)
+
+
+def test_empty_and_k_tail(gpu):
+    x = torch.zeros(0, 64, dtype=torch.float16, device=gpu)
+    q = torch.zeros(32, 64, dtype=torch.int8, device=gpu)
+    assert ra.int8_gemm(x, q, torch.ones(32, device=gpu)).shape == (0, 32)
+    for (M, K, N) in [(1, 4096 + 16, 128), (3, 1040, 100), (300, 4096 + 48, 256), (260, 4096 + 64, 300)]:
+        c = gemm_case(M, K, N, seed=K)
+        for v in (GEMV, SKINNY, TILED):
+            y = _run(c.x.to(gpu), c.q.to(gpu), c.s.to(gpu), None, v)
+            if y is None:
+                assert v == GEMV and M > 4
+                continue
+            _oracle_check(y.cpu(), c.x, c.q, c.s)
+
+
+def test_graph_replay_matches_eager(gpu):
+    c = gemm_case(1, 4096, 11008, seed=2, device=gpu)
+    eager = ra.int8_gemm(c.x, c.q, c.s)
+    torch.cuda.synchronize()
+    out = {}
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ra.int8_gemm(c.x, c.q, c.s)        # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out["y"] = ra.int8_gemm(c.x, c.q, c.s)
+    for i in range(3):
+        out["y"].zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out["y"], eager), f"replay {i}"

@@ -1,0 +1,166 @@
+"""GPU parity of the decoder-MLP path kernels and the weight quantiser.
+
+* quantize_weight_per_channel on the GPU == the oracle, bit for bit (fp32
+  closed form incl. ties / zero rows; fp16 / bf16 golden vectors).
+* rmsnorm / swiglu_fused vs the oracle (reference fallback restated).
+* fused gate/up + SwiGLU vs int8_gemm + swiglu and vs the oracle.
+* the bf16 MLP workload (H=8192, I=28672, M in {1, 17, 4096}) vs an fp32
+  torch reference of the fallback composition on the GPU.
+"""
+import numpy as np
+import pytest
+import torch
+
+import rotalabs_accel as ra
+from oracle import fallback
+from oracle import quant as oq
+from workloads import MLP_SHAPES, mlp_case
+
+pytestmark = pytest.mark.gpu
+
+
+def _t16(bits, dt):
+    return torch.from_numpy(bits.astype(np.int16)).view(dt)
+
+
+def test_quantize_fp32_bit_exact(gpu):
+    g = torch.Generator().manual_seed(5)
+    w = torch.randn(300, 1000, generator=g) * 0.02
+    w[0] = 0
+    w[1] = 0
+    w[1, :9] = torch.tensor([127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -125.5])
+    w[2] *= 1e-35                      # subnormal scales
+    w[3] = torch.linspace(-3, 3, 1000)
+    print("  quantize fp32 [300,1000]", flush=True)
+    q, s = ra.quantize_weight_per_channel(w.to(gpu))
+    q_o, s_o = oq.quantize_weight_per_channel(w.numpy())
+    assert np.array_equal(q.cpu().numpy(), q_o)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_o.view(np.uint32))
+
+
+@pytest.mark.parametrize("name,dt", [("f16", torch.float16), ("bf16", torch.bfloat16)])
+def test_quantize_reduced_bit_exact(gpu, golden, name, dt):
+    w = _t16(golden[f"qpc_{name}_w"], dt)
+    q, s = ra.quantize_weight_per_channel(w.to(gpu))
+    assert np.array_equal(q.cpu().numpy(), golden[f"qpc_{name}_q"])
+    assert np.array_equal(s.cpu().numpy(), golden[f"qpc_{name}_s"])
+
+
+def test_quantize_large_matches_cpu(gpu):
+    g = torch.Generator().manual_seed(6)
+    w = torch.randn(4096, 4096, generator=g) * 0.02
+    q, s = ra.quantize_weight_per_channel(w.to(gpu))
+    q_c, s_c = ra.quantize_weight_per_channel(w)
+    assert torch.equal(q.cpu(), q_c) and torch.equal(s.cpu(), s_c)
+
+
+@pytest.mark.parametrize("xdt,wdt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                     (torch.float16, torch.float32), (torch.float32, torch.float32)])
+def test_rmsnorm_vs_oracle(gpu, xdt, wdt):
+    g = torch.Generator().manual_seed(7)
+    x = (torch.randn(33, 8192, generator=g) * 2).to(xdt)
+    w = (1 + 0.01 * torch.randn(8192, generator=g)).to(wdt)
+    print(f"  rmsnorm {xdt} {wdt}", flush=True)
+    y = ra.rmsnorm(x.to(gpu), w.to(gpu), 1e-6).cpu()
+    ref = fallback.rmsnorm_ref(x, w, 1e-6)
+    assert y.dtype == ref.dtype
+    torch.testing.assert_close(y.float(), ref.float(), rtol=1e-2, atol=1e-2)
+    if y.dtype != torch.float32:
+        # all but a sliver of 16-bit outputs are bit-identical (the mean's
+        # summation order differs, which can move a rounding boundary)
+        assert (y == ref).float().mean() > 0.99
+
+
+def test_rmsnorm_golden(gpu, golden):
+    x = _t16(golden["rms_x_bf16"], torch.bfloat16)
+    w = _t16(golden["rms_w_bf16"], torch.bfloat16)
+    y = ra.rmsnorm(x.to(gpu), w.to(gpu)).cpu()
+    ref = _t16(golden["rms_y_bf16"], torch.bfloat16)
+    torch.testing.assert_close(y.float(), ref.float(), rtol=1e-2, atol=1e-2)
+    assert (y == ref).float().mean() > 0.98
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+def test_swiglu_vs_oracle(gpu, dt):
+    g = torch.Generator().manual_seed(8)
+    a = (torch.randn(17, 3001, generator=g) * 3).to(dt)
+    b = torch.randn(17, 3001, generator=g).to(dt)
+    y = ra.swiglu_fused(a.to(gpu), b.to(gpu)).cpu()
+    ref64 = fallback.swiglu_f64(a.float().numpy(), b.float().numpy())
+    np.testing.assert_allclose(y.double().numpy(), ref64, rtol=1e-2 if dt != torch.float32 else 1e-5,
+                               atol=1e-2 if dt != torch.float32 else 1e-6)
+    torch.testing.assert_close(y.float(), fallback.swiglu_ref(a, b).float(), rtol=1e-2, atol=1e-2)
+
+
+def _round(a64, dt):
+    return torch.from_numpy(a64).to(dt).double().numpy()
+
+
+def _swiglu_chain64(g64, u64, dt):
+    """The reference composition's roundings on exact (float64) gate/up sums:
+    gate, up stored in dt; silu(gate) stored in dt; product stored in dt."""
+    g, u = _round(g64, dt), _round(u64, dt)
+    return _round(_round(g / (1.0 + np.exp(-g)), dt) * u, dt)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,K,inter", [(1, 1024, 512), (5, 512, 300), (17, 2048, 640), (64, 256, 128),
+                                        (100, 512, 96), (300, 1024, 200)])
+def test_gateup_swiglu_vs_oracle(gpu, dt, M, K, inter):
+    g = torch.Generator().manual_seed(M + K)
+    x = torch.randn(M, K, generator=g).to(dt)
+    q, s = ra.quantize_weight_per_channel(torch.randn(2 * inter, K, generator=g) * 0.02)
+    print(f"  gateup M={M} K={K} I={inter} {dt}", flush=True)
+    h = ra.int8_gateup_swiglu(x.to(gpu), q.to(gpu), s.to(gpu)).cpu()
+    assert h.shape == (M, inter) and h.dtype == dt
+    # fp32-accumulated reference (exact sums) with the composition's roundings
+    y64 = fallback.gemm_f64(x.float().numpy(), q.numpy(), s.numpy())
+    ref = _swiglu_chain64(y64[:, :inter], y64[:, inter:], dt)
+    err = np.abs(h.double().numpy() - ref)
+    assert (err <= 1e-2 + 1e-2 * np.abs(ref)).all(), err.max()
+    # a rounding boundary can move by one ulp at most in a few outputs
+    assert (err == 0).mean() > 0.99
+    ulp = 2.0 ** -10 if dt == torch.float16 else 2.0 ** -7
+    assert (err <= 2 * ulp * np.maximum(np.abs(ref), 1e-3) + 1e-6).all()
+    # the unfused GPU composition (int8_gemm then swiglu_fused) agrees too
+    gu = ra.int8_gemm(x.to(gpu), q.to(gpu), s.to(gpu))
+    h2 = ra.swiglu_fused(gu[:, :inter].contiguous(), gu[:, inter:].contiguous()).cpu()
+    torch.testing.assert_close(h.float(), h2.float(), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("M,H,I,seed", MLP_SHAPES)
+def test_mlp_workload_full_size(gpu, M, H, I, seed):
+    """bf16 decoder MLP at H=8192, I=28672 against the fp32-accumulated
+    reference of the composition (RMSNorm -> gate/up -> SwiGLU -> down with
+    the fallback's activation roundings, weights = fp32 q*s, float64 sums),
+    on the GPU."""
+    print(f"  mlp M={M} H={H} I={I}", flush=True)
+    c = mlp_case(M, H, I, seed, device=gpu)
+    y = ra.int8_mlp(c.x, c.norm_w, c.q_gu, c.s_gu, c.q_d, c.s_d, 1e-6)
+    torch.cuda.synchronize()
+    assert y.shape == (M, H) and y.dtype == torch.bfloat16
+    xf = c.x.float()
+    h_ref = ((xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16) * c.norm_w)
+    h = ra.rmsnorm(c.x, c.norm_w, 1e-6)
+    torch.testing.assert_close(h.float(), h_ref.float(), rtol=1e-2, atol=1e-2)
+    # float64 GEMMs: the reference must not add rounding of its own
+    w = (c.q_gu.float() * c.s_gu[:, None]).double().t().contiguous()
+    gu = h_ref.double() @ w
+    del w
+    gb, ub = gu[:, :I].to(torch.bfloat16), gu[:, I:].to(torch.bfloat16)
+    a = (torch.nn.functional.silu(gb) * ub)                 # bf16 ops: silu, product each rounded
+    del gu
+    wd = (c.q_d.float() * c.s_d[:, None]).double().t().contiguous()
+    y_ref = (a.double() @ wd).float()
+    del wd
+    err = (y.float() - y_ref).abs()
+    assert bool((err <= 1e-2 + 1e-2 * y_ref.abs()).all()), f"max err {err.max().item()}"
+    # the module gives the same result
+    mlp = ra.Int8SwiGLUMLP(H, I).to(gpu)
+    mlp.weight_gate_up.copy_(c.q_gu)
+    mlp.scale_gate_up.copy_(c.s_gu)
+    mlp.weight_down.copy_(c.q_d)
+    mlp.scale_down.copy_(c.s_d)
+    mlp.norm_weight.data.copy_(c.norm_w)
+    mlp._quantized = True
+    assert torch.equal(mlp(c.x), y)

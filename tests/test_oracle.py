@@ -1,0 +1,191 @@
+"""The oracle is pinned before it is trusted (CPU only).
+
+* fp32 per-channel quantization: numpy closed form == independent C
+  restatement, bit for bit; invariants; round-half-even tie rows; row
+  independence; brute force on tiny inputs.
+* fp16/bf16 quantization, int8_gemm_torch outputs, quantization-error
+  metrics, rmsnorm_torch, swiglu_torch: golden vectors from the reference.
+* GEMM: the float64 reference equals a brute-force triple loop (C) and exact
+  known answers (integer inputs, power-of-two scales).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cquant, fallback
+from oracle import quant as oq
+
+
+def _edge_rows(rng, rows=48, cols=96):
+    w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    w[0] = 0
+    w[1] = 0
+    w[1, 3] = -0.5
+    w[2] = np.linspace(-1, 1, cols, dtype=np.float32)
+    w[3] = 0
+    w[3, 0] = 127.0
+    w[3, 1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -125.5]
+    w[4] *= 1e-30
+    w[5, :] = 3.0
+    return w
+
+
+def test_fp32_quant_numpy_equals_c():
+    rng = np.random.default_rng(0)
+    for shape in [(48, 96), (7, 1), (1, 4096), (33, 1000)]:
+        w = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+        q1, s1 = oq.quantize_weight_per_channel(w)
+        q2, s2 = cquant.quantize_rows_f32(w)
+        assert np.array_equal(q1, q2) and np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
+    w = _edge_rows(rng)
+    q1, s1 = oq.quantize_weight_per_channel(w)
+    q2, s2 = cquant.quantize_rows_f32(w)
+    assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+
+
+def test_fp32_quant_invariants_and_ties():
+    rng = np.random.default_rng(1)
+    w = _edge_rows(rng)
+    q, s = oq.quantize_weight_per_channel(w)
+    assert q.dtype == np.int8 and s.dtype == np.float32 and q.shape == w.shape and s.shape == (w.shape[0],)
+    assert np.abs(q.astype(np.int32)).max() <= 127
+    # zero row -> scale 1, q 0
+    assert s[0] == 1.0 and not q[0].any()
+    # scale is the single fp32 rounding of max/127
+    amax = np.abs(w).max(axis=1)
+    expect = (amax / np.float32(127)).astype(np.float32)
+    expect[expect == 0] = 1
+    assert np.array_equal(s, expect)
+    # the row maximum maps to +-127
+    for r in range(1, w.shape[0]):
+        k = np.argmax(np.abs(w[r]))
+        if amax[r] / np.float32(127) > 0:
+            assert abs(int(q[r, k])) == 127
+    # row 3: max 127 -> s == 1 exactly; ties round half to even
+    assert s[3] == 1.0
+    assert q[3, 1:9].tolist() == [0, 2, 2, 0, -2, -2, 126, -126]
+    # constant row -> all 127
+    assert (q[5] == 127).all()
+
+
+def test_fp32_quant_row_independence():
+    rng = np.random.default_rng(2)
+    a = (rng.standard_normal((20, 64)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal((30, 64)) * 0.02).astype(np.float32)
+    qa, sa = oq.quantize_weight_per_channel(a)
+    qb, sb = oq.quantize_weight_per_channel(b)
+    qc, sc = oq.quantize_weight_per_channel(np.concatenate([a, b]))
+    assert np.array_equal(qc, np.concatenate([qa, qb])) and np.array_equal(sc, np.concatenate([sa, sb]))
+
+
+def test_fp32_quant_brute_force():
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((5, 7)) * 0.1).astype(np.float32)
+    q, s = oq.quantize_weight_per_channel(w)
+    for r in range(5):
+        m = max(abs(float(v)) for v in w[r])
+        sr = float(np.float32(np.float32(m) / np.float32(127)))
+        assert s[r] == np.float32(sr)
+        for k in range(7):
+            v = float(np.float32(w[r, k] / np.float32(sr)))
+            rq = int(np.rint(v))  # numpy rint: half to even
+            assert q[r, k] == max(-128, min(127, rq))
+
+
+@pytest.mark.parametrize("name", ["f16", "bf16"])
+def test_reduced_precision_quant_golden(golden, name):
+    wb = golden[f"qpc_{name}_w"]
+    w32 = wb.view(np.float16).astype(np.float32) if name == "f16" else oq.bf16_bits_to_f32(wb)
+    q, s = oq.quantize_weight_per_channel(w32, name)
+    assert np.array_equal(q, golden[f"qpc_{name}_q"])
+    assert np.array_equal(s, golden[f"qpc_{name}_s"])
+    qt, st = oq.quantize_symmetric(w32, name)
+    assert np.array_equal(qt, golden[f"qpt_{name}_q"])
+    assert np.array_equal(np.atleast_1d(st), golden[f"qpt_{name}_s"])
+
+
+def test_quant_error_metrics_golden(golden):
+    x = golden["qerr_x"]
+    q, s = oq.quantize_symmetric(x)
+    e = oq.calculate_quantization_error(x, q, s)
+    got = [e["max_abs_error"], e["mean_abs_error"], e["relative_error_pct"], e["snr_db"]]
+    np.testing.assert_allclose(got, golden["qerr_vals"], rtol=1e-5)
+    q2, s2 = oq.quantize_weight_per_channel(x)
+    e2 = oq.calculate_quantization_error(x, q2, s2, dim=0)
+    got2 = [e2["max_abs_error"], e2["mean_abs_error"], e2["relative_error_pct"], e2["snr_db"]]
+    np.testing.assert_allclose(got2, golden["qerr_pc_vals"], rtol=1e-5)
+
+
+def _t16(bits, dt):
+    return torch.from_numpy(bits.astype(np.int16)).view(dt)
+
+
+@pytest.mark.parametrize("name,dt", [("f16", torch.float16), ("bf16", torch.bfloat16), ("f32", torch.float32)])
+def test_int8_gemm_fallback_golden(golden, name, dt):
+    x = torch.from_numpy(golden["gemm_x_f32"]).to(dt)
+    q = torch.from_numpy(golden["gemm_q"])
+    s = torch.from_numpy(golden["gemm_s"])
+    b = torch.from_numpy(golden["gemm_b_f32"]).to(dt)
+    y = fallback.int8_gemm_ref(x, q, s)
+    yb = fallback.int8_gemm_ref(x, q, s, b)
+    if dt == torch.float32:
+        assert np.array_equal(y.numpy(), golden["gemm_y_f32"])
+        assert np.array_equal(yb.numpy(), golden["gemm_yb_f32"])
+    else:
+        assert torch.equal(y, _t16(golden[f"gemm_y_{name}"], dt))
+        assert torch.equal(yb, _t16(golden[f"gemm_yb_{name}"], dt))
+
+
+def test_reference_unit_case_golden(golden):
+    x = torch.from_numpy(golden["reftest_x"])
+    w = torch.from_numpy(golden["reftest_w"])
+    y = fallback.int8_gemm_ref(x, w, torch.ones(128))
+    assert y.shape == (2, 8, 128)
+    assert np.array_equal(y.numpy(), golden["reftest_y"])
+
+
+def test_rmsnorm_swiglu_golden(golden):
+    x = _t16(golden["rms_x_bf16"], torch.bfloat16)
+    w = _t16(golden["rms_w_bf16"], torch.bfloat16)
+    assert torch.equal(fallback.rmsnorm_ref(x, w), _t16(golden["rms_y_bf16"], torch.bfloat16))
+    xh = _t16(golden["rms_x_f16"], torch.float16)
+    wf = torch.from_numpy(golden["rms_w_f32"])
+    y = fallback.rmsnorm_ref(xh, wf)
+    assert y.dtype == torch.float32
+    assert np.array_equal(y.numpy(), golden["rms_y_f16w32"])
+    g = _t16(golden["swiglu_g_bf16"], torch.bfloat16)
+    u = _t16(golden["swiglu_u_bf16"], torch.bfloat16)
+    assert torch.equal(fallback.swiglu_ref(g, u), _t16(golden["swiglu_y_bf16"], torch.bfloat16))
+
+
+def test_gemm_f64_equals_brute_force():
+    rng = np.random.default_rng(4)
+    for (M, K, N) in [(1, 48, 43), (17, 64, 5), (3, 16, 16)]:
+        x = rng.standard_normal((M, K))
+        q = rng.integers(-127, 128, (N, K)).astype(np.int8)
+        s = (rng.random(N).astype(np.float32) * 0.01 + 1e-3).astype(np.float32)
+        np.testing.assert_allclose(fallback.gemm_f64(x, q, s), cquant.w8a16_gemm_f64(x, q, s), rtol=1e-12, atol=1e-12)
+
+
+def test_gemm_known_answer():
+    # integer x, scale = 2^-e: every partial sum is an exact small integer
+    rng = np.random.default_rng(5)
+    M, K, N = 4, 64, 8
+    x = rng.integers(-2, 3, (M, K)).astype(np.float64)
+    q = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    s = np.full(N, 0.25, np.float32)
+    exact = (x.astype(np.int64) @ q.astype(np.int64).T) * 0.25
+    assert np.array_equal(fallback.gemm_f64(x, q, s), exact)
+    # scale == 1 reduces to the integer product
+    assert np.array_equal(fallback.gemm_f64(x, q, np.ones(N, np.float32)), exact * 4)
+
+
+def test_dequantize_closed_form():
+    rng = np.random.default_rng(6)
+    q = rng.integers(-128, 128, (16, 32)).astype(np.int8)
+    s = (rng.random(16) * 0.05).astype(np.float32)
+    ref = fallback.dequantize_ref(torch.from_numpy(q), torch.from_numpy(s), torch.float16)
+    mine = oq.dequantize(q, s, "f16")
+    assert np.array_equal(ref.float().numpy(), mine)
+    refb = fallback.dequantize_ref(torch.from_numpy(q), torch.from_numpy(s), torch.bfloat16)
+    assert np.array_equal(refb.float().numpy(), oq.dequantize(q, s, "bf16"))
