@@ -226,7 +226,7 @@ def main():
                         f"N(0,0.02) (seed {seed}), {N_COPIES} resident weight copies cycled per step",
             "M": M, "K": K, "N": N,
             "bytes_per_step": dbytes,
-            "kernel_variant": {1: "skinny", 2: "tiled", 3: "generic", 4: "gemv"}.get(variant, str(variant)),
+            "kernel_variant": {1: "skinny", 2: "tiled", 3: "generic", 4: "gemv", 5: "rows"}.get(variant, str(variant)),
             "timing": "HIP graph of 120 launches replayed; HIP events on the launch stream",
             "host_launched_us_per_step": round(ms_eager * 1e3, 3),
         },
@@ -237,7 +237,7 @@ def main():
         "prefill": {
             "metric": "int8_gemm TFLOP/s @M=2048 K=4096 N=11008",
             "value": round(tflops, 1), "unit": "TFLOP/s", "ms_per_step": pms, "steps": args.prefill_steps,
-            "kernel_variant": {1: "skinny", 2: "tiled", 3: "generic", 4: "gemv"}.get(pvariant, str(pvariant)),
+            "kernel_variant": {1: "skinny", 2: "tiled", 3: "generic", 4: "gemv", 5: "rows"}.get(pvariant, str(pvariant)),
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_FP16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4), "traffic": None},
         },

@@ -15,6 +15,17 @@ int to_status(hipError_t e) { return e == hipSuccess ? RA_OK : RA_ERR_LAUNCH; }
 SkinnyCfg g_skinny_override{0, 0, 0};
 #endif
 
+}  // namespace
+
+#ifdef RA_TUNING
+namespace ra {
+int g_tiled_mode = 0;
+int g_rows_rw = 0;
+}
+#endif
+
+namespace {
+
 SkinnyCfg skinny_config(int64_t M, int64_t N, int64_t K) {
   SkinnyCfg c = skinny_select(M, N, K);
 #ifdef RA_TUNING
@@ -29,6 +40,7 @@ constexpr int64_t kSkinnyMaxM = 64;
 
 int select_variant(const GemmArgs &a) {
   if (a.K == 0) return RA_VARIANT_GENERIC;
+  if (gemv_rows_supported(a)) return RA_VARIANT_ROWS;
   if (gemv_supported(a)) return RA_VARIANT_GEMV;
   if (a.M <= kSkinnyMaxM && skinny_supported(a)) return RA_VARIANT_SKINNY;
   if (tiled_supported(a)) return RA_VARIANT_TILED;
@@ -53,6 +65,8 @@ extern "C" {
 
 #ifdef RA_TUNING
 void ra_tune_skinny(int mt, int rt, int nw) { g_skinny_override = SkinnyCfg{mt, rt, nw}; }
+void ra_tune_tiled(int mode) { ra::g_tiled_mode = mode; }
+void ra_tune_rows(int rw) { ra::g_rows_rw = rw; }
 #endif
 
 int ra_abi_version(void) { return RA_ABI_VERSION; }
@@ -82,6 +96,9 @@ int ra_w8a16_gemm_ex(const void *x, int64_t ldx, int x_dtype, const int8_t *w, i
     case RA_VARIANT_SKINNY:
       if (!skinny_supported(a) || K == 0) return RA_ERR_VARIANT;
       return to_status(skinny_launch(a, skinny_config(M, N, K), s));
+    case RA_VARIANT_ROWS:
+      if (!gemv_rows_supported(a)) return RA_ERR_VARIANT;
+      return to_status(gemv_rows_launch(a, s));
     case RA_VARIANT_GEMV:
       if (!gemv_supported(a)) return RA_ERR_VARIANT;
       return to_status(gemv_launch(a, s));
@@ -119,6 +136,7 @@ int ra_w8a16_gateup_swiglu(const void *x, int64_t ldx, int x_dtype, const int8_t
   if (ldx < K || ldw < K || ldh < I) return RA_ERR_ARG;
   const GateUpArgs a{x, ldx, x_dtype, w, ldw, scale, h, ldh, M, I, K};
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (K > 0 && gateup_gemv_rows_supported(a)) return to_status(gateup_gemv_rows_launch(a, s));
   if (K > 0 && gateup_gemv_supported(a)) return to_status(gateup_gemv_launch(a, s));
   if (K > 0 && M <= kSkinnyMaxM && gateup_skinny_supported(a)) return to_status(gateup_skinny_launch(a, s));
   if (K > 0 && gateup_tiled_supported(a)) return to_status(gateup_tiled_launch(a, s));

@@ -1,0 +1,254 @@
+// Row GEMV for decode (M <= 2) on gfx950: one weight row per wave, VALU dot
+// products, no LDS, no barriers.
+//
+// Replaces the reference's Triton tile loop (src/rotalabs_accel/kernels/
+// gemm.py:113-138) for the decode shapes, where the whole cost is streaming
+// N*K weight bytes from HBM. Measured on MI355X, a CU sustains only a bounded
+// number of outstanding 128-byte line requests, so the kernel time is set by
+// the bytes assigned to the busiest CU: the work must be split into many
+// small, equal, independent units that the hardware dispatcher balances
+// across CUs as they finish. Here the unit is one weight row per wave:
+//
+//  * Lane l reads bytes 16l .. 16l+15 of each 1 KB window of its row (one
+//    128-bit load per window, the whole wave reading 1 KB contiguous = 8 full
+//    128-byte lines); CH windows are loaded at once, with the matching
+//    activation chunks x[m][k .. k+15] (two 128-bit loads, L2 resident).
+//  * int8 -> fp16 is exact (magic-number conversion) and the products are
+//    accumulated with v_dot2_f32_f16 (two fp16 products per instruction, fp32
+//    accumulator); bf16 converts through fp32 (exact) and uses
+//    v_dot2_f32_bf16. Per weight: 1.75 VALU ops (fp16), 2 (bf16).
+//  * A wave64 reduction gives the row's dot product; scale (+ bias), or the
+//    SwiGLU of the gate/up pair, is applied to the fp32 sum before the single
+//    rounding. Deterministic; no workspace.
+#include "ra_common.h"
+#include "ra_internal.h"
+
+namespace ra {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kRowsMaxM = 2;
+constexpr int kRowsCh = 4;  // windows of 1 KB in flight per wave
+
+// sum += dot(x[0..15], q[0..15]) for 16 weights packed in w (4 dwords) and 16
+// activations in xa (elements 0..7) and xb (8..15).
+template <int DT>
+__device__ __forceinline__ float dot16(const uint4 &w, const uint4 &xa, const uint4 &xb, float sum);
+
+template <>
+__device__ __forceinline__ float dot16<RA_F16>(const uint4 &w, const uint4 &xa, const uint4 &xb, float sum) {
+  const uint4 lo = dq8_f16(w.x, w.y), hi = dq8_f16(w.z, w.w);
+  sum = __builtin_amdgcn_fdot2(bitcast<f16x2>(lo.x), bitcast<f16x2>(xa.x), sum, false);
+  sum = __builtin_amdgcn_fdot2(bitcast<f16x2>(lo.y), bitcast<f16x2>(xa.y), sum, false);
+  sum = __builtin_amdgcn_fdot2(bitcast<f16x2>(lo.z), bitcast<f16x2>(xa.z), sum, false);
+  sum = __builtin_amdgcn_fdot2(bitcast<f16x2>(lo.w), bitcast<f16x2>(xa.w), sum, false);
+  sum = __builtin_amdgcn_fdot2(bitcast<f16x2>(hi.x), bitcast<f16x2>(xb.x), sum, false);
+  sum = __builtin_amdgcn_fdot2(bitcast<f16x2>(hi.y), bitcast<f16x2>(xb.y), sum, false);
+  sum = __builtin_amdgcn_fdot2(bitcast<f16x2>(hi.z), bitcast<f16x2>(xb.z), sum, false);
+  sum = __builtin_amdgcn_fdot2(bitcast<f16x2>(hi.w), bitcast<f16x2>(xb.w), sum, false);
+  return sum;
+}
+
+template <>
+__device__ __forceinline__ float dot16<RA_BF16>(const uint4 &w, const uint4 &xa, const uint4 &xb, float sum) {
+  const uint4 lo = dq8_bf16(w.x, w.y), hi = dq8_bf16(w.z, w.w);
+  sum = __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(lo.x), bitcast<bf16x2>(xa.x), sum, false);
+  sum = __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(lo.y), bitcast<bf16x2>(xa.y), sum, false);
+  sum = __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(lo.z), bitcast<bf16x2>(xa.z), sum, false);
+  sum = __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(lo.w), bitcast<bf16x2>(xa.w), sum, false);
+  sum = __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(hi.x), bitcast<bf16x2>(xb.x), sum, false);
+  sum = __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(hi.y), bitcast<bf16x2>(xb.y), sum, false);
+  sum = __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(hi.z), bitcast<bf16x2>(xb.z), sum, false);
+  sum = __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(hi.w), bitcast<bf16x2>(xb.w), sum, false);
+  return sum;
+}
+
+// One wave per RW consecutive output rows n0 .. n0+RW-1 (with GU: gate rows n
+// and up rows N + n). The RW rows are loaded together and share the wave's
+// activation loads, which are L2 hits but cost the CU as many line requests
+// as the weight loads themselves.
+template <int DT, int MR, int RW, bool GU>
+__global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t *__restrict__ x, int64_t ldx,
+                                                        const int8_t *__restrict__ w, int64_t ldw,
+                                                        const float *__restrict__ scale,
+                                                        const void *__restrict__ bias, int bias_dt,
+                                                        uint16_t *__restrict__ y, int64_t ldy, int M, int N,
+                                                        int K) {
+  using A = Act<DT>;
+  constexpr int NR = GU ? 2 * RW : RW;  // weight rows per wave: [r] gate/plain, [RW + r] up
+  const int lane = threadIdx.x & 63;
+  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RW;
+  if (n0 >= N) return;  // whole wave; no barriers in this kernel
+  // Rows past N (last wave only) are clamped to N - 1: in bounds, never stored.
+  const int8_t *wr[NR];
+#pragma unroll
+  for (int t = 0; t < NR; ++t) {
+    const int n = min(n0 + t % RW, N - 1);
+    wr[t] = w + (int64_t)(t < RW ? n : N + n) * ldw + 16 * lane;
+  }
+  const uint16_t *xr[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) xr[m] = x + (int64_t)(m < M ? m : 0) * ldx + 16 * lane;
+
+  float acc[NR][MR];
+#pragma unroll
+  for (int t = 0; t < NR; ++t)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[t][m] = 0.f;
+
+  // Main loop: kRowsCh whole windows, unconditional 128-bit loads (a guarded
+  // load would be split into per-dword loads, each waited on). x rows m >= M
+  // alias row 0 and their sums are never stored.
+  int k0 = 0;
+  for (; k0 + 1024 * kRowsCh <= K; k0 += 1024 * kRowsCh) {
+    uint4 wv[kRowsCh][NR], xa[kRowsCh][MR], xb[kRowsCh][MR];
+#pragma unroll
+    for (int c = 0; c < kRowsCh; ++c)
+#pragma unroll
+      for (int t = 0; t < NR; ++t) wv[c][t] = *reinterpret_cast<const uint4 *>(wr[t] + k0 + 1024 * c);
+#pragma unroll
+    for (int c = 0; c < kRowsCh; ++c)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        xa[c][m] = *reinterpret_cast<const uint4 *>(xr[m] + k0 + 1024 * c);
+        xb[c][m] = *reinterpret_cast<const uint4 *>(xr[m] + k0 + 1024 * c + 8);
+      }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the step is issued before the first wait
+#pragma unroll
+    for (int c = 0; c < kRowsCh; ++c)
+#pragma unroll
+      for (int t = 0; t < NR; ++t)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[t][m] = dot16<DT>(wv[c][t], xa[c][m], xb[c][m], acc[t][m]);
+  }
+  // Tail: single windows; K % 16 == 0, so a lane's 16-byte chunk is all in or
+  // all out. Lanes past K re-read the first 16 elements of their rows
+  // (offset -16*lane from their own column; K >= 16) and contribute zeros.
+  for (; k0 < K; k0 += 1024) {
+    const bool ok = k0 + 16 * lane + 16 <= K;
+    const int k = ok ? k0 : -16 * lane;
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    uint4 wv[NR], xa[MR], xb[MR];
+#pragma unroll
+    for (int t = 0; t < NR; ++t) {
+      wv[t] = *reinterpret_cast<const uint4 *>(wr[t] + k);
+      if (!ok) wv[t] = z;
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      xa[m] = *reinterpret_cast<const uint4 *>(xr[m] + k);
+      xb[m] = *reinterpret_cast<const uint4 *>(xr[m] + k + 8);
+      if (!ok) xa[m] = xb[m] = z;
+    }
+#pragma unroll
+    for (int t = 0; t < NR; ++t)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) acc[t][m] = dot16<DT>(wv[t], xa[m], xb[m], acc[t][m]);
+  }
+
+  // Reduce over the wave; lane r stores row n0 + r.
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const float s0 = wave_sum(acc[r][m]);
+      const float s1 = GU ? wave_sum(acc[NR - RW + r][m]) : 0.f;
+      const int n = n0 + r;
+      if (lane == r && m < M && n < N) {
+        uint16_t *yrow = y + (int64_t)m * ldy;
+        if (GU)
+          yrow[n] = swiglu_out<A>(s0 * scale[n], s1 * scale[N + n]);
+        else
+          yrow[n] = A::out(epilogue_value(s0, scale, bias, bias_dt, n));
+      }
+    }
+  }
+}
+
+static bool rows_ok(int x_dt, const void *x, int64_t ldx, const int8_t *w, int64_t ldw, int64_t M, int64_t N,
+                    int64_t K) {
+  if (x_dt != RA_F16 && x_dt != RA_BF16) return false;
+  if (M < 1 || M > kRowsMaxM || N > ((int64_t)1 << 30) || K < 16 || K % 16 != 0 || K > ((int64_t)1 << 30))
+    return false;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w) & 15)) return false;
+  return (ldx % 8) == 0 && (ldw % 16) == 0;
+}
+
+bool gemv_rows_supported(const GemmArgs &a) { return rows_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.M, a.N, a.K); }
+
+bool gateup_gemv_rows_supported(const GateUpArgs &a) {
+  return rows_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.M, a.I, a.K);
+}
+
+// Rows per wave: as many as keep >= kRowsMinWaves waves in the grid (the
+// dispatcher balances CUs only with many small units), at most 4.
+constexpr int kRowsMinWaves = 4096;
+
+static int rows_per_wave(int64_t M, int64_t N, bool gu) {
+  const int cap = (gu || M > 1) ? 2 : 4;
+  int rw = cap;
+  while (rw > 1 && N / rw < kRowsMinWaves) rw >>= 1;
+#ifdef RA_TUNING
+  extern int g_rows_rw;  // 0 auto, else forced rows per wave (capped)
+  if (g_rows_rw > 0) rw = g_rows_rw < cap ? g_rows_rw : cap;
+#endif
+  return rw;
+}
+
+struct RowsParams {
+  const uint16_t *x;
+  int64_t ldx;
+  const int8_t *w;
+  int64_t ldw;
+  const float *scale;
+  const void *bias;
+  int bias_dt;
+  uint16_t *y;
+  int64_t ldy;
+  int M, N, K;
+};
+
+template <int DT, int MR, int RW, bool GU>
+static void rows_go(const RowsParams &p, hipStream_t s) {
+  const int64_t waves = ((int64_t)p.N + RW - 1) / RW;
+  hipLaunchKernelGGL((gemv_rows_kernel<DT, MR, RW, GU>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p.x,
+                     p.ldx, p.w, p.ldw, p.scale, p.bias, p.bias_dt, p.y, p.ldy, p.M, p.N, p.K);
+}
+
+template <int DT, int MR, bool GU>
+static void rows_go_rw(const RowsParams &p, int rw, hipStream_t s) {
+  if constexpr (MR == 1 && !GU) {
+    if (rw == 4) return rows_go<DT, MR, 4, GU>(p, s);
+  }
+  if (rw >= 2) return rows_go<DT, MR, 2, GU>(p, s);
+  rows_go<DT, MR, 1, GU>(p, s);
+}
+
+template <bool GU>
+static hipError_t rows_launch(const void *x, int64_t ldx, int x_dt, const int8_t *w, int64_t ldw,
+                              const float *scale, const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M,
+                              int64_t N, int64_t K, hipStream_t s) {
+  const RowsParams p{static_cast<const uint16_t *>(x), ldx, w, ldw, scale, bias, bias_dt,
+                     static_cast<uint16_t *>(y), ldy, (int)M, (int)N, (int)K};
+  const int rw = rows_per_wave(M, N, GU);
+  if (x_dt == RA_F16) {
+    if (M == 1) rows_go_rw<RA_F16, 1, GU>(p, rw, s);
+    else rows_go_rw<RA_F16, 2, GU>(p, rw, s);
+  } else {
+    if (M == 1) rows_go_rw<RA_BF16, 1, GU>(p, rw, s);
+    else rows_go_rw<RA_BF16, 2, GU>(p, rw, s);
+  }
+  return hipGetLastError();
+}
+
+hipError_t gemv_rows_launch(const GemmArgs &a, hipStream_t s) {
+  return rows_launch<false>(a.x, a.ldx, a.x_dt, a.w, a.ldw, a.scale, a.bias, a.bias_dt, a.y, a.ldy, a.M, a.N, a.K,
+                            s);
+}
+
+hipError_t gateup_gemv_rows_launch(const GateUpArgs &a, hipStream_t s) {
+  return rows_launch<true>(a.x, a.ldx, a.x_dt, a.w, a.ldw, a.scale, nullptr, RA_F32, a.h, a.ldh, a.M, a.I, a.K,
+                           s);
+}
+
+}  // namespace ra

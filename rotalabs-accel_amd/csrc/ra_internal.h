@@ -56,6 +56,12 @@ bool gateup_tiled_supported(const GateUpArgs &a);
 hipError_t gateup_tiled_launch(const GateUpArgs &a, hipStream_t s);
 hipError_t gateup_generic_launch(const GateUpArgs &a, hipStream_t s);
 
+// Row GEMV (M <= 2): one weight row per wave, VALU dot products.
+bool gemv_rows_supported(const GemmArgs &a);
+hipError_t gemv_rows_launch(const GemmArgs &a, hipStream_t s);
+bool gateup_gemv_rows_supported(const GateUpArgs &a);
+hipError_t gateup_gemv_rows_launch(const GateUpArgs &a, hipStream_t s);
+
 // Decode GEMV (M <= 4, x staged in LDS, one HBM round trip per wave).
 bool gemv_supported(const GemmArgs &a);
 hipError_t gemv_launch(const GemmArgs &a, hipStream_t s);

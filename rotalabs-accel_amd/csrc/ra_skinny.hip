@@ -53,12 +53,10 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
     wp[t] = w + (int64_t)n * ldw + 16 * g;
   }
   const uint16_t *xp[MT];
-  bool xv[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = m0 + 16 * mt + r;
-    xv[mt] = m < M;
-    xp[mt] = x + (int64_t)(xv[mt] ? m : 0) * ldx + 16 * g;
+    xp[mt] = x + (int64_t)(m < M ? m : 0) * ldx + 16 * g;
   }
 
   f32x4 acc[NTW][MT];
@@ -83,13 +81,11 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        if (xv[mt]) {
-          xa[u][mt] = *reinterpret_cast<const uint4 *>(xp[mt] + k + 64 * u);
-          xb[u][mt] = *reinterpret_cast<const uint4 *>(xp[mt] + k + 64 * u + 8);
-        } else {
-          xa[u][mt] = zero4;
-          xb[u][mt] = zero4;
-        }
+        // Unconditional: rows m >= M alias row 0 and only feed MFMA columns
+        // that are never stored (a guarded load would be split into waited
+        // per-dword loads).
+        xa[u][mt] = *reinterpret_cast<const uint4 *>(xp[mt] + k + 64 * u);
+        xb[u][mt] = *reinterpret_cast<const uint4 *>(xp[mt] + k + 64 * u + 8);
       }
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -105,17 +101,23 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
       }
   }
   // Remaining steps, one at a time; a lane group whose 16 k's lie beyond K
-  // (only possible in the last step, K % 16 == 0) contributes zeros.
+  // (only possible in the last step, K % 16 == 0) re-reads the first 16
+  // elements of its rows (offset -16*g from its own column; K >= 16) and
+  // contributes zeros.
   for (; k < ke; k += 64) {
     const bool gv = k + 16 * g + 16 <= K;
+    const int kk = gv ? k : -16 * g;
     uint4 wv[NTW], xa[MT], xb[MT];
 #pragma unroll
-    for (int t = 0; t < NTW; ++t) wv[t] = gv ? *reinterpret_cast<const uint4 *>(wp[t] + k) : zero4;
+    for (int t = 0; t < NTW; ++t) {
+      wv[t] = *reinterpret_cast<const uint4 *>(wp[t] + kk);
+      if (!gv) wv[t] = zero4;
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const bool ok = gv && xv[mt];
-      xa[mt] = ok ? *reinterpret_cast<const uint4 *>(xp[mt] + k) : zero4;
-      xb[mt] = ok ? *reinterpret_cast<const uint4 *>(xp[mt] + k + 8) : zero4;
+      xa[mt] = *reinterpret_cast<const uint4 *>(xp[mt] + kk);
+      xb[mt] = *reinterpret_cast<const uint4 *>(xp[mt] + kk + 8);
+      if (!gv) xa[mt] = xb[mt] = zero4;
     }
 #pragma unroll
     for (int t = 0; t < NTW; ++t) {

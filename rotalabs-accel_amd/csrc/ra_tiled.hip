@@ -12,10 +12,13 @@
 //    registers while tile k is multiplied out of LDS, then written to the
 //    other buffer; one barrier per K tile.
 //  * A (activations) in LDS: 256 rows x 128 B, 16-byte chunks XOR-swizzled by
-//    (row & 7) so the MFMA operand reads (8 consecutive rows, same chunk) hit
-//    all banks once.
+//    ((row >> 1) & 7). LDS serves a 128-bit access 16 lanes per cycle (64
+//    banks x 4 B), so the MFMA operand reads (16 consecutive rows, same
+//    chunk) must land in 16 distinct 16-byte bank groups: rows alternate
+//    between the two 128-byte halves of a 256-byte bank row, and the swizzle
+//    separates the 8 rows within each half.
 //  * B (weights) stays int8 in LDS (8 KB per stage: half the LDS traffic of
-//    fp16), 128 rows x 64 B, 8-byte chunks swizzled by ((row >> 1) & 7); each
+//    fp16), 128 rows x 64 B, 8-byte chunks swizzled by ((row >> 2) & 7); each
 //    wave dequantises its 32x16 B fragments in registers right before the
 //    MFMA (exact int8 -> fp16/bf16).
 //  * K permutation: in sub-step s (0..3) lane group g (0,1) supplies the 8
@@ -87,7 +90,7 @@ __global__ __launch_bounds__(256, 2) void tiled_kernel(const uint16_t *__restric
     int gr = m0 + row;
     gr = gr < M ? gr : M - 1;
     ap[i] = x + (int64_t)gr * ldx + ac * 8;
-    a_off[i] = row * 128 + ((ac ^ (row & 7)) << 4);
+    a_off[i] = row * 128 + ((ac ^ ((row >> 1) & 7)) << 4);
   }
   // B: 2 x 16 B per thread: rows i*64 + tid/4, bytes 16*(tid%4) .. +15
   // (= 8-byte chunks 2q and 2q+1).
@@ -109,7 +112,7 @@ __global__ __launch_bounds__(256, 2) void tiled_kernel(const uint16_t *__restric
       wr = wr < N ? wr : N - 1;
     }
     bp[i] = w + (int64_t)wr * ldw + bq * 16;
-    const int sw = (row >> 1) & 7;
+    const int sw = (row >> 2) & 7;
     b_off0[i] = A_BYTES + row * 64 + (((2 * bq) ^ sw) << 3);
     b_off1[i] = A_BYTES + row * 64 + (((2 * bq + 1) ^ sw) << 3);
   }
@@ -138,11 +141,11 @@ __global__ __launch_bounds__(256, 2) void tiled_kernel(const uint16_t *__restric
                   *reinterpret_cast<uint2 *>(base_ + b_off1[i]) = make_uint2(rb[i].z, rb[i].w);) \
   }
 
-  // ---- MFMA operand read offsets (row & 7 == lane & 7 for A rows) ----
+  // ---- MFMA operand read offsets (row bases are multiples of 32) ----
   const int a_row_base = (wm * 128 + l32) * 128;
   const int b_row_base = A_BYTES + (wn * 64 + l32) * 64;
-  const int a_sw = lane & 7;
-  const int b_sw = (lane >> 1) & 7;
+  const int a_sw = (l32 >> 1) & 7;
+  const int b_sw = (l32 >> 2) & 7;
 
   f32x16 acc[4][2];
 #pragma unroll
@@ -287,23 +290,24 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
   const int l32 = lane & 31, g = lane >> 5;
 
   // ---- copy sources: A copy i covers tile rows 8*ai .. +7 (ai = 8*wid + i),
-  // lane -> row 8*ai + lane/8, LDS chunk lane%8 <- global chunk (lane%8)^(row&7)
+  // lane -> row 8*ai + lane/8, LDS chunk lane%8 <- global chunk
+  // (lane%8) ^ ((row>>1)&7)
   const uint16_t *a_src[A_COPIES];
 #pragma unroll
   for (int i = 0; i < A_COPIES; ++i) {
     const int row = 8 * (A_COPIES * wid + i) + (lane >> 3);
-    const int c = (lane & 7) ^ (row & 7);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
     int gr = m0 + row;
     gr = gr < M ? gr : M - 1;
     a_src[i] = x + (int64_t)gr * ldx + c * 8;
   }
   // B copy i covers tile rows 16*bi .. +15 (bi = 2*wid + i), lane -> row
-  // 16*bi + lane/4, LDS chunk lane%4 <- global chunk (lane%4)^((row>>1)&3)
+  // 16*bi + lane/4, LDS chunk lane%4 <- global chunk (lane%4)^((row>>2)&3)
   const int8_t *b_src[B_COPIES];
 #pragma unroll
   for (int i = 0; i < B_COPIES; ++i) {
     const int row = 16 * (B_COPIES * wid + i) + (lane >> 2);
-    const int c = (lane & 3) ^ ((row >> 1) & 3);
+    const int c = (lane & 3) ^ ((row >> 2) & 3);
     int wr;
     if (GU) {
       const int half = (row >> 5) & 1, jj = row & 31;
@@ -340,49 +344,88 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
 
   const int a_row_off = (wm * 128 + l32) * 128;
   const int b_row_off = A_BYTES + (wn * 64 + l32) * 64;
-  const int a_sw = l32 & 7;
-  const int b_sw = (l32 >> 1) & 3;
+  const int a_sw = (l32 >> 1) & 7;
+  const int b_sw = (l32 >> 2) & 3;
+
+  // Software pipeline at sub-step granularity. A fragments ping-pong between
+  // two sets (sub-step ss+1 is read while ss is multiplied); B (both pairs of
+  // the tile, 4 x 16 B) is read once per tile into the set of the tile after.
+  // The tile boundary (wait for the next tile's copies, barrier, next copy,
+  // first reads of the next tile) sits before the last sub-step's MFMAs.
+  uint4 fa0[4], fa1[4], fbA[2][2], fbB[2][2];
+#define RA_READ_A(st_, ss_, FA)                                                                     \
+  {                                                                                                 \
+    const uint8_t *base_ = lds + (st_) * STAGE;                                                     \
+    _Pragma("unroll") for (int bi = 0; bi < 4; ++bi) FA[bi] = *reinterpret_cast<const uint4 *>(     \
+        base_ + a_row_off + bi * 32 * 128 + (((4 * ((ss_) >> 1) + 2 * g + ((ss_) & 1)) ^ a_sw) << 4)); \
+  }
+#define RA_READ_B(st_, FB)                                                                          \
+  {                                                                                                 \
+    const uint8_t *base_ = lds + (st_) * STAGE;                                                     \
+    _Pragma("unroll") for (int p = 0; p < 2; ++p)                                                   \
+        _Pragma("unroll") for (int bj = 0; bj < 2; ++bj) FB[p][bj] = *reinterpret_cast<const uint4 *>( \
+            base_ + b_row_off + bj * 32 * 64 + (((2 * p + g) ^ b_sw) << 4));                        \
+  }
+#define RA_MMA(ss_, FA, FB)                                                                         \
+  {                                                                                                 \
+    uint4 bf_[2];                                                                                   \
+    _Pragma("unroll") for (int bj = 0; bj < 2; ++bj) bf_[bj] = ((ss_) & 1)                          \
+        ? Ac::dq8(FB[(ss_) >> 1][bj].z, FB[(ss_) >> 1][bj].w)                                        \
+        : Ac::dq8(FB[(ss_) >> 1][bj].x, FB[(ss_) >> 1][bj].y);                                       \
+    _Pragma("unroll") for (int bi = 0; bi < 4; ++bi)                                                \
+        _Pragma("unroll") for (int bj = 0; bj < 2; ++bj) acc[bi][bj] =                              \
+            Ac::mfma32(FA[bi], bf_[bj], acc[bi][bj]);                                               \
+  }
+// One K tile kt_ from B set FBC (A sub-step 0 already in fa0). Before the last
+// sub-step: complete this tile's LDS reads, wait until this wave's copies of
+// tile kt_+1 are done (only younger tiles in flight), barrier (tile kt_+1 is
+// visible to all; stage kt_ % S is free), copy tile kt_+S into it, and start
+// reading tile kt_+1 (A sub-step 0 into fa0, B into FBN).
+#define RA_TILE(kt_, FBC, FBN)                                                                        \
+  {                                                                                                   \
+    const int st_ = (kt_) % S;                                                                        \
+    RA_READ_A(st_, 1, fa1);                                                                           \
+    RA_MMA(0, fa0, FBC);                                                                              \
+    RA_READ_A(st_, 2, fa0);                                                                           \
+    RA_MMA(1, fa1, FBC);                                                                              \
+    RA_READ_A(st_, 3, fa1);                                                                           \
+    RA_MMA(2, fa0, FBC);                                                                              \
+    if ((kt_) + 1 < KT) {                                                                             \
+      const int younger_ = min(KT - 2 - (kt_), S - 2);                                                \
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                              \
+      if (younger_ >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * COPIES) : "memory");            \
+      else if (younger_ == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(COPIES) : "memory");           \
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");                                           \
+      asm volatile("s_barrier" ::: "memory");                                                         \
+      if ((kt_) + S < KT) RA_ISSUE((kt_) + S, st_);                                                   \
+      RA_READ_A(((kt_) + 1) % S, 0, fa0);                                                             \
+      RA_READ_B(((kt_) + 1) % S, FBN);                                                                \
+    }                                                                                                 \
+    RA_MMA(3, fa1, FBC);                                                                              \
+  }
 
   const int KT = K / BK;
 #pragma unroll
-  for (int s = 0; s < S - 1; ++s)
+  for (int s = 0; s < S; ++s)
     if (s < KT) RA_ISSUE(s, s);
-  for (int kt = 0; kt < KT; ++kt) {
-    // copies of tiles kt+1 .. kt+S-2 (those issued) may stay in flight
-    const int younger = min(S - 2, KT - 1 - kt);
-    if (younger >= 2) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * COPIES) : "memory");
-    } else if (younger == 1) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(COPIES) : "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
+  {
+    const int younger0 = min(KT, S) - 1;  // tiles issued after tile 0
+    if (younger0 >= 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * COPIES) : "memory");
+    else if (younger0 == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * COPIES) : "memory");
+    else if (younger0 == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(COPIES) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     asm volatile("s_barrier" ::: "memory");
-    if (kt + S - 1 < KT) RA_ISSUE(kt + S - 1, (kt + S - 1) % S);
-    const uint8_t *base = lds + (kt % S) * STAGE;
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      uint4 braw[2];
-#pragma unroll
-      for (int bj = 0; bj < 2; ++bj)
-        braw[bj] = *reinterpret_cast<const uint4 *>(base + b_row_off + bj * 32 * 64 + (((2 * p + g) ^ b_sw) << 4));
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int a = 4 * p + 2 * g + h;
-        uint4 af[4], bf[2];
-#pragma unroll
-        for (int bi = 0; bi < 4; ++bi)
-          af[bi] = *reinterpret_cast<const uint4 *>(base + a_row_off + bi * 32 * 128 + ((a ^ a_sw) << 4));
-#pragma unroll
-        for (int bj = 0; bj < 2; ++bj)
-          bf[bj] = h ? Ac::dq8(braw[bj].z, braw[bj].w) : Ac::dq8(braw[bj].x, braw[bj].y);
-#pragma unroll
-        for (int bi = 0; bi < 4; ++bi)
-#pragma unroll
-          for (int bj = 0; bj < 2; ++bj) acc[bi][bj] = Ac::mfma32(af[bi], bf[bj], acc[bi][bj]);
-      }
-    }
   }
+  RA_READ_A(0, 0, fa0);
+  RA_READ_B(0, fbA);
+  for (int kt = 0; kt < KT; kt += 2) {
+    RA_TILE(kt, fbA, fbB);
+    if (kt + 1 < KT) RA_TILE(kt + 1, fbB, fbA);
+  }
+#undef RA_TILE
+#undef RA_MMA
+#undef RA_READ_B
+#undef RA_READ_A
 #undef RA_ISSUE
 
   // ---- epilogue (as tiled_kernel) ----
@@ -437,7 +480,13 @@ static hipError_t launch(const void *x, int64_t ldx, int x_dt, const int8_t *w, 
   const int tiles_m = (int)((M + tiled::BM - 1) / tiled::BM);
   const int tiles_n = (int)((N + OUTN - 1) / OUTN);
   const dim3 grid((unsigned)(tiles_m * tiles_n));
-  if (K % tiled::BK == 0) {
+#ifdef RA_TUNING
+  extern int g_tiled_mode;  // 0 auto, 1 register-staged kernel, 2 direct-to-LDS kernel
+  const bool use_dma = g_tiled_mode == 2 || (g_tiled_mode == 0 && K % tiled::BK == 0);
+#else
+  const bool use_dma = K % tiled::BK == 0;
+#endif
+  if (use_dma) {
     constexpr int S = RA_TILED_STAGES;
     if (x_dt == RA_F16)
       hipLaunchKernelGGL((tiled_dma_kernel<RA_F16, GU, S>), grid, dim3(256), 0, s,
