@@ -50,7 +50,46 @@ def parse():
     p.add_argument("--prefill-steps", type=int, default=60)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--only", choices=("all", "decode", "prefill"), default="all",
+                   help="run one workload only (for profiler runs)")
+    p.add_argument("--no-graph", action="store_true",
+                   help="time host-launched loops instead of HIP graph replay (for counter runs)")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run a plain 256 MiB device copy (torch copy_), the known-size kernel that "
+                        "scales FETCH_SIZE / WRITE_SIZE counter readings to bytes")
     return p.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(HERE, "profiles", "hbm_traffic.md")
+
+
+def measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of ``kernel`` on ``workload`` as measured by the
+    rocprofv3 FETCH_SIZE + WRITE_SIZE runs recorded in profiles/hbm_traffic.md
+    (table rows ``| workload | kernel | algorithmic B | fetch B | write B |
+    traffic B |``); None when no row matches."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) >= 6 and cells[0] == workload and cells[1] == kernel:
+                    return int(cells[5].replace(",", ""))
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def copy_calibration():
+    """A plain device copy of 256 MiB, five times: reads and writes exactly
+    268,435,456 bytes per launch."""
+    import torch
+    n = 256 * 2**20 // 2
+    src = torch.randn(n, device="cuda:0").half()
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: 5 copies of {n * 2} bytes")
 
 
 class GemmLauncher:
@@ -140,29 +179,19 @@ def cpu_baseline(M, K, N, seed, budget_s):
             "gbs": gemm_bytes(M, K, N) / med / 1e9, "tflops": gemm_flops(M, K, N) / med / 1e12}
 
 
-def main():
-    args = parse()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
-              "multi-GPU sharding is design-only.", file=sys.stderr)
-        sys.exit(2)
+VARIANT_NAMES = {1: "skinny", 2: "tiled", 3: "generic", 4: "gemv", 5: "rows"}
+# Kernel (symbol prefix in rocprofv3 traces) that each variant launches.
+VARIANT_KERNELS = {1: "skinny_kernel", 2: "tiled_dma_kernel", 3: "generic_kernel", 4: "gemv_kernel",
+                   5: "gemv_rows_kernel"}
 
+
+def run_decode(args, dev):
+    """Decode M=1: returns (ms/step graph or host loop, ms/step host loop,
+    GB/s, timed steps, variant)."""
     import torch
     import rotalabs_accel as ra
     from rotalabs_accel import _backend
-    from workloads import gemm_bytes, gemm_case, gemm_flops
-
-    if not torch.cuda.is_available():
-        print("bench.py: no GPU visible", file=sys.stderr)
-        sys.exit(1)
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    _backend.load()
-    props = torch.cuda.get_device_properties(dev)
-    log(f"device {props.name} ({getattr(props, 'gcnArchName', '?')}), {props.multi_processor_count} CUs")
-
-    # ---------------- decode M=1 (headline) ----------------
+    from workloads import gemm_bytes, gemm_case
     M, K, N, seed = DECODE
     c = gemm_case(M, K, N, seed, device=dev)
     copies = [c.q] + [c.q.clone() for _ in range(N_COPIES - 1)]
@@ -177,14 +206,22 @@ def main():
     log(f"decode M={M} K={K} N={N}: variant {variant}, {N_COPIES} weight copies "
         f"({N_COPIES * N * K / 2**20:.0f} MiB), warmup {args.warmup}, steps {args.steps}")
     ms_eager = time_eager(launcher, min(args.steps, 2000), args.warmup)
-    ms, timed_steps = time_graph(launcher, args.steps, args.warmup, per_graph=10 * N_COPIES)
-    dbytes = gemm_bytes(M, K, N)
-    gbs = dbytes / (ms * 1e-3) / 1e9
-    log(f"decode: {ms * 1e3:.2f} us/step in graph replay, {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%} of HBM peak); "
-        f"host-launched loop {ms_eager * 1e3:.2f} us/step")
-    del launcher, copies
+    if args.no_graph:
+        ms, timed_steps = ms_eager, min(args.steps, 2000)
+    else:
+        ms, timed_steps = time_graph(launcher, args.steps, args.warmup, per_graph=10 * N_COPIES)
+    gbs = gemm_bytes(M, K, N) / (ms * 1e-3) / 1e9
+    log(f"decode: {ms * 1e3:.2f} us/step ({'host loop' if args.no_graph else 'graph replay'}), {gbs:.0f} GB/s "
+        f"({gbs / PEAK_HBM_GBS:.1%} of HBM peak); host-launched loop {ms_eager * 1e3:.2f} us/step")
+    return ms, ms_eager, gbs, timed_steps, variant
 
-    # ---------------- prefill M=2048 ----------------
+
+def run_prefill(args, dev):
+    """Prefill M=2048: returns (ms/step, TFLOP/s, variant)."""
+    import torch
+    import rotalabs_accel as ra
+    from rotalabs_accel import _backend
+    from workloads import gemm_case, gemm_flops
     Mp, Kp, Np, seedp = PREFILL
     cp = gemm_case(Mp, Kp, Np, seedp, device=dev)
     yp = torch.empty((Mp, Np), dtype=torch.float16, device=dev)
@@ -195,11 +232,56 @@ def main():
     torch.cuda.synchronize()
     assert torch.equal(yp, pref), "timed prefill path differs from int8_gemm"
     pvariant = _backend.load().ra_w8a16_gemm_select(Mp, Np, Kp, _backend.F16)
-    pms, _ = time_graph(plaunch, args.prefill_steps, 3, per_graph=3 * len(pcopies))
+    if args.no_graph:
+        pms = time_eager(plaunch, args.prefill_steps, 3)
+    else:
+        pms, _ = time_graph(plaunch, args.prefill_steps, 3, per_graph=3 * len(pcopies))
     tflops = gemm_flops(Mp, Kp, Np) / (pms * 1e-3) / 1e12
-    log(f"prefill M={Mp}: variant {pvariant}, {pms * 1e3:.1f} us/step, {tflops:.0f} TFLOP/s "
+    log(f"prefill M={Mp} K={Kp} N={Np}: variant {pvariant}, {pms * 1e3:.1f} us/step, {tflops:.0f} TFLOP/s "
         f"({tflops / PEAK_FP16_TFLOPS:.1%} of dense fp16 peak)")
-    del plaunch, pcopies
+    return pms, tflops, pvariant
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
+              "multi-GPU sharding is design-only.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from rotalabs_accel import _backend
+    from workloads import gemm_bytes
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        copy_calibration()
+        return
+    _backend.load()
+    props = torch.cuda.get_device_properties(dev)
+    log(f"device {props.name} ({getattr(props, 'gcnArchName', '?')}), {props.multi_processor_count} CUs")
+
+    # ---------------- decode M=1 (headline) ----------------
+    M, K, N, seed = DECODE
+    ms = ms_eager = gbs = float("nan")
+    timed_steps, variant = 0, None
+    if args.only in ("all", "decode"):
+        ms, ms_eager, gbs, timed_steps, variant = run_decode(args, dev)
+    dbytes = gemm_bytes(M, K, N)
+
+    # ---------------- prefill M=2048 ----------------
+    Mp, Kp, Np, seedp = PREFILL
+    pms = tflops = float("nan")
+    pvariant = None
+    if args.only in ("all", "prefill"):
+        pms, tflops, pvariant = run_prefill(args, dev)
+    if args.only != "all":
+        return
 
     # ---------------- CPU baseline ----------------
     cpu = None
@@ -226,20 +308,24 @@ def main():
                         f"N(0,0.02) (seed {seed}), {N_COPIES} resident weight copies cycled per step",
             "M": M, "K": K, "N": N,
             "bytes_per_step": dbytes,
-            "kernel_variant": {1: "skinny", 2: "tiled", 3: "generic", 4: "gemv", 5: "rows"}.get(variant, str(variant)),
-            "timing": "HIP graph of 120 launches replayed; HIP events on the launch stream",
+            "kernel_variant": VARIANT_NAMES.get(variant, str(variant)),
+            "timing": ("host-launched loop" if args.no_graph else
+                       "HIP graph of 120 launches replayed") + "; HIP events on the launch stream",
             "host_launched_us_per_step": round(ms_eager * 1e3, 3),
         },
         "roofline": {
             "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+            "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "traffic": measured_traffic(f"decode M={M} K={K} N={N}", VARIANT_KERNELS.get(variant, "")),
         },
         "prefill": {
             "metric": "int8_gemm TFLOP/s @M=2048 K=4096 N=11008",
             "value": round(tflops, 1), "unit": "TFLOP/s", "ms_per_step": pms, "steps": args.prefill_steps,
-            "kernel_variant": {1: "skinny", 2: "tiled", 3: "generic", 4: "gemv", 5: "rows"}.get(pvariant, str(pvariant)),
+            "kernel_variant": VARIANT_NAMES.get(pvariant, str(pvariant)),
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_FP16_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4), "traffic": None},
+                         "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
+                         "traffic": measured_traffic(f"prefill M={Mp} K={Kp} N={Np}",
+                                                     VARIANT_KERNELS.get(pvariant, ""))},
         },
     }
     if cpu is not None:
