@@ -38,10 +38,6 @@
 
 namespace ra {
 
-#ifndef RA_TILED_STAGES
-#define RA_TILED_STAGES 4
-#endif
-
 namespace tiled {
 constexpr int BM = 256, BN = 128, BK = 64;
 constexpr int A_BYTES = BM * BK * 2;  // 32 KB
@@ -255,19 +251,57 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t lds_wave_base) {
                : "memory", "m0");
 }
 
-template <int DT, bool GU, int S>
+// Tile geometry of the direct-to-LDS kernel: 4 waves in a 2 x 2 grid, each
+// owning BMB x BNB blocks of 32 x 32 outputs (one v_mfma_f32_32x32x16 per
+// block and 16-deep K sub-step). Bigger per-wave tiles need fewer LDS bytes
+// per MFMA: (4,2) reads 0.625 KB per MFMA, (3,4) 0.417, (4,4) 0.375.
+template <int BMB, int BNB>
+struct DmaTile {
+  static constexpr int WM = 32 * BMB, WN = 32 * BNB;  // per-wave sub-tile
+  static constexpr int BM = 2 * WM, BN = 2 * WN, BK = 64;
+  static constexpr int A_BYTES = BM * BK * 2;  // fp16/bf16 rows of 128 B
+  static constexpr int B_BYTES = BN * BK;      // int8 rows of 64 B
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int A_COPIES = A_BYTES / 4096;  // 1 KB copies per wave per K tile
+  static constexpr int B_COPIES = B_BYTES / 4096;
+  static constexpr int COPIES = A_COPIES + B_COPIES;
+  static constexpr int S = (160 * 1024) / STAGE < 4 ? (160 * 1024) / STAGE : 4;  // pipeline depth
+  static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "copies must split evenly over 4 waves");
+  static_assert(S >= 2 && S <= 4, "2 to 4 stages");
+  static_assert((S - 1) * COPIES <= 63, "vmcnt is a 6-bit counter");
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Wait until at most `younger` K tiles of copies (COPIES loads each) are
+// still in flight for this wave; younger <= S - 1 <= 3.
+template <int COPIES>
+__device__ __forceinline__ void wait_tiles(int younger) {
+  if (younger >= 3) wait_vmcnt<3 * COPIES>();
+  else if (younger == 2) wait_vmcnt<2 * COPIES>();
+  else if (younger == 1) wait_vmcnt<COPIES>();
+  else wait_vmcnt<0>();
+}
+
+template <int DT, bool GU, int BMB, int BNB>
 __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__restrict__ x, int64_t ldx,
                                                            const int8_t *__restrict__ w, int64_t ldw,
                                                            const float *__restrict__ scale,
                                                            const void *__restrict__ bias, int bias_dt,
                                                            uint16_t *__restrict__ y, int64_t ldy, int M, int N,
                                                            int K, int tiles_m, int tiles_n) {
-  using namespace tiled;
+  using G = DmaTile<BMB, BNB>;
   using Ac = Act<DT>;
+  constexpr int BM = G::BM, BN = G::BN, BK = G::BK, WM = G::WM, WN = G::WN, S = G::S;
+  constexpr int A_COPIES = G::A_COPIES, B_COPIES = G::B_COPIES, COPIES = G::COPIES;
+  constexpr int STAGE = G::STAGE, A_BYTES = G::A_BYTES;
+  // GU: each wave's WN weight rows are WN/2 gate rows followed by the WN/2
+  // matching up rows, so block bj (< BNB/2) pairs with block bj + BNB/2.
+  static_assert(!GU || BNB % 2 == 0, "gate/up pairing needs an even number of column blocks");
   constexpr int OUTN = GU ? BN / 2 : BN;
-  constexpr int A_COPIES = A_BYTES / 1024 / 4;  // per wave per tile: 8
-  constexpr int B_COPIES = B_BYTES / 1024 / 4;  // 2
-  constexpr int COPIES = A_COPIES + B_COPIES;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE];
 
   // ---- tile coordinates (XCD-aware, grouped along M; as tiled_kernel) ----
@@ -289,9 +323,9 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
   const int wm = wid >> 1, wn = wid & 1;
   const int l32 = lane & 31, g = lane >> 5;
 
-  // ---- copy sources: A copy i covers tile rows 8*ai .. +7 (ai = 8*wid + i),
-  // lane -> row 8*ai + lane/8, LDS chunk lane%8 <- global chunk
-  // (lane%8) ^ ((row>>1)&7)
+  // ---- copy sources: A copy i covers tile rows 8*ai .. +7 (ai = A_COPIES*wid
+  // + i), lane -> row 8*ai + lane/8, LDS chunk lane%8 <- global chunk
+  // (lane%8) ^ ((row>>1)&7). Rows past M are clamped (loaded, never stored).
   const uint16_t *a_src[A_COPIES];
 #pragma unroll
   for (int i = 0; i < A_COPIES; ++i) {
@@ -301,8 +335,8 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
     gr = gr < M ? gr : M - 1;
     a_src[i] = x + (int64_t)gr * ldx + c * 8;
   }
-  // B copy i covers tile rows 16*bi .. +15 (bi = 2*wid + i), lane -> row
-  // 16*bi + lane/4, LDS chunk lane%4 <- global chunk (lane%4)^((row>>2)&3)
+  // B copy i covers tile rows 16*bi .. +15 (bi = B_COPIES*wid + i), lane ->
+  // row 16*bi + lane/4, LDS chunk lane%4 <- global chunk (lane%4)^((row>>2)&3).
   const int8_t *b_src[B_COPIES];
 #pragma unroll
   for (int i = 0; i < B_COPIES; ++i) {
@@ -310,8 +344,8 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
     const int c = (lane & 3) ^ ((row >> 2) & 3);
     int wr;
     if (GU) {
-      const int half = (row >> 5) & 1, jj = row & 31;
-      int j = n0 + (row >> 6) * 32 + jj;
+      const int rr = row % WN, half = rr / (WN / 2);
+      int j = n0 + (row / WN) * (WN / 2) + rr % (WN / 2);
       j = j < N ? j : N - 1;
       wr = half ? N + j : j;
     } else {
@@ -334,125 +368,172 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
         dma16(b_src[i] + kofs_, b_dst + so_ + (uint32_t)i * 1024);                         \
   }
 
-  f32x16 acc[4][2];
+  f32x16 acc[BMB][BNB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < BMB; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < BNB; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int a_row_off = (wm * 128 + l32) * 128;
-  const int b_row_off = A_BYTES + (wn * 64 + l32) * 64;
+  // Rows of this lane's fragments: A row wm*WM + 32*bi + l32, B row
+  // wn*WN + 32*bj + l32; the swizzle terms reduce to l32 because WM/2 and
+  // WN/4 are multiples of 8 and 4.
+  const int a_row_off = (wm * WM + l32) * 128;
+  const int b_row_off = A_BYTES + (wn * WN + l32) * 64;
   const int a_sw = (l32 >> 1) & 7;
   const int b_sw = (l32 >> 2) & 3;
 
-  // Software pipeline at sub-step granularity. A fragments ping-pong between
-  // two sets (sub-step ss+1 is read while ss is multiplied); B (both pairs of
-  // the tile, 4 x 16 B) is read once per tile into the set of the tile after.
-  // The tile boundary (wait for the next tile's copies, barrier, next copy,
-  // first reads of the next tile) sits before the last sub-step's MFMAs.
-  uint4 fa0[4], fa1[4], fbA[2][2], fbB[2][2];
+  // Software pipeline at sub-step granularity (4 sub-steps of 16 k per K
+  // tile), with the order pinned by scheduling barriers so that LDS latency
+  // and dequantisation hide under the MFMAs:
+  //   sub-step ss: [LDS reads for ss+1] | [MFMAs of ss, interleaved 1:1 with
+  //   the dequantisation of ss+1's B fragments]
+  // A fragments ping-pong in fa[2]; the raw 16-byte B fragments of sub-step
+  // pair p sit in fbr[p] (pair 1 is read during sub-step 0, pair 0 of the
+  // next tile during sub-step 3); dequantised B ping-pongs in bq[2]. The tile
+  // boundary (wait for the next tile's copies, barrier, next copy, first
+  // reads of the next tile) opens sub-step 3.
+  uint4 fa[2][BMB], fbr[2][BNB], bq[2][BNB];
 #define RA_READ_A(st_, ss_, FA)                                                                     \
   {                                                                                                 \
     const uint8_t *base_ = lds + (st_) * STAGE;                                                     \
-    _Pragma("unroll") for (int bi = 0; bi < 4; ++bi) FA[bi] = *reinterpret_cast<const uint4 *>(     \
+    _Pragma("unroll") for (int bi = 0; bi < BMB; ++bi) FA[bi] = *reinterpret_cast<const uint4 *>(   \
         base_ + a_row_off + bi * 32 * 128 + (((4 * ((ss_) >> 1) + 2 * g + ((ss_) & 1)) ^ a_sw) << 4)); \
   }
-#define RA_READ_B(st_, FB)                                                                          \
+#define RA_READ_B(st_, p_, FB)                                                                      \
   {                                                                                                 \
     const uint8_t *base_ = lds + (st_) * STAGE;                                                     \
-    _Pragma("unroll") for (int p = 0; p < 2; ++p)                                                   \
-        _Pragma("unroll") for (int bj = 0; bj < 2; ++bj) FB[p][bj] = *reinterpret_cast<const uint4 *>( \
-            base_ + b_row_off + bj * 32 * 64 + (((2 * p + g) ^ b_sw) << 4));                        \
+    _Pragma("unroll") for (int bj = 0; bj < BNB; ++bj) FB[bj] = *reinterpret_cast<const uint4 *>(   \
+        base_ + b_row_off + bj * 32 * 64 + (((2 * (p_) + g) ^ b_sw) << 4));                         \
   }
-#define RA_MMA(ss_, FA, FB)                                                                         \
+#define RA_DEQ(h_, FB, BQ)                                                                          \
+  _Pragma("unroll") for (int bj = 0; bj < BNB; ++bj) BQ[bj] =                                       \
+      (h_) ? Ac::dq8(FB[bj].z, FB[bj].w) : Ac::dq8(FB[bj].x, FB[bj].y);
+#define RA_MMA(FA, BQ)                                                                              \
+  _Pragma("unroll") for (int bi = 0; bi < BMB; ++bi)                                                \
+      _Pragma("unroll") for (int bj = 0; bj < BNB; ++bj) acc[bi][bj] = Ac::mfma32(FA[bi], BQ[bj], acc[bi][bj]);
+// Interleave the BMB*BNB MFMAs with the dequantisation VALU work.
+#define RA_INTERLEAVE()                                                                             \
+  _Pragma("unroll") for (int i_ = 0; i_ < BMB * BNB; ++i_) {                                        \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                              \
+    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);                                              \
+  }                                                                                                 \
+  __builtin_amdgcn_sched_barrier(0);
+// Sub-step 3: the dequantisation needs B fragments read at the start of the
+// sub-step, so the first half of the MFMAs runs before it.
+#define RA_INTERLEAVE_LATE()                                                                        \
+  __builtin_amdgcn_sched_group_barrier(0x008, (BMB * BNB) / 2, 0);                                  \
+  _Pragma("unroll") for (int i_ = 0; i_ < BMB * BNB - (BMB * BNB) / 2; ++i_) {                      \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                              \
+    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);                                              \
+  }                                                                                                 \
+  __builtin_amdgcn_sched_barrier(0);
+// Sub-steps 0..2 of the tile in stage st_.
+#define RA_SUBSTEPS_012(st_)                                                                        \
+  RA_READ_A(st_, 1, fa[1]);                                                                         \
+  RA_READ_B(st_, 1, fbr[1]);                                                                        \
+  __builtin_amdgcn_sched_barrier(0);                                                                \
+  RA_MMA(fa[0], bq[0]);                                                                             \
+  RA_DEQ(1, fbr[0], bq[1]);                                                                         \
+  RA_INTERLEAVE();                                                                                  \
+  RA_READ_A(st_, 2, fa[0]);                                                                         \
+  __builtin_amdgcn_sched_barrier(0);                                                                \
+  RA_MMA(fa[1], bq[1]);                                                                             \
+  RA_DEQ(0, fbr[1], bq[0]);                                                                         \
+  RA_INTERLEAVE();                                                                                  \
+  RA_READ_A(st_, 3, fa[1]);                                                                         \
+  __builtin_amdgcn_sched_barrier(0);                                                                \
+  RA_MMA(fa[0], bq[0]);                                                                             \
+  RA_DEQ(1, fbr[1], bq[1]);                                                                         \
+  RA_INTERLEAVE();
+// Tile boundary + sub-step 3: this tile's LDS reads are complete; wait until
+// only the copies of tiles younger than kt_+1 are in flight, then the barrier
+// makes tile kt_+1 visible and frees stage st_ for tile kt_+S, whose copies
+// are issued (ISSUE_); then the first reads of tile kt_+1 and the last MFMAs
+// of tile kt_, with the dequantisation of tile kt_+1's first B fragments.
+#define RA_BOUNDARY_SUBSTEP3(kt_, st_, YOUNGER_, ISSUE_)                                            \
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                                \
+  wait_tiles<COPIES>(YOUNGER_);                                                                     \
+  asm volatile("s_barrier" ::: "memory");                                                           \
+  if (ISSUE_) RA_ISSUE((kt_) + S, st_);                                                             \
   {                                                                                                 \
-    uint4 bf_[2];                                                                                   \
-    _Pragma("unroll") for (int bj = 0; bj < 2; ++bj) bf_[bj] = ((ss_) & 1)                          \
-        ? Ac::dq8(FB[(ss_) >> 1][bj].z, FB[(ss_) >> 1][bj].w)                                        \
-        : Ac::dq8(FB[(ss_) >> 1][bj].x, FB[(ss_) >> 1][bj].y);                                       \
-    _Pragma("unroll") for (int bi = 0; bi < 4; ++bi)                                                \
-        _Pragma("unroll") for (int bj = 0; bj < 2; ++bj) acc[bi][bj] =                              \
-            Ac::mfma32(FA[bi], bf_[bj], acc[bi][bj]);                                               \
-  }
-// One K tile kt_ from B set FBC (A sub-step 0 already in fa0). Before the last
-// sub-step: complete this tile's LDS reads, wait until this wave's copies of
-// tile kt_+1 are done (only younger tiles in flight), barrier (tile kt_+1 is
-// visible to all; stage kt_ % S is free), copy tile kt_+S into it, and start
-// reading tile kt_+1 (A sub-step 0 into fa0, B into FBN).
-#define RA_TILE(kt_, FBC, FBN)                                                                        \
-  {                                                                                                   \
-    const int st_ = (kt_) % S;                                                                        \
-    RA_READ_A(st_, 1, fa1);                                                                           \
-    RA_MMA(0, fa0, FBC);                                                                              \
-    RA_READ_A(st_, 2, fa0);                                                                           \
-    RA_MMA(1, fa1, FBC);                                                                              \
-    RA_READ_A(st_, 3, fa1);                                                                           \
-    RA_MMA(2, fa0, FBC);                                                                              \
-    if ((kt_) + 1 < KT) {                                                                             \
-      const int younger_ = min(KT - 2 - (kt_), S - 2);                                                \
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                              \
-      if (younger_ >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * COPIES) : "memory");            \
-      else if (younger_ == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(COPIES) : "memory");           \
-      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");                                           \
-      asm volatile("s_barrier" ::: "memory");                                                         \
-      if ((kt_) + S < KT) RA_ISSUE((kt_) + S, st_);                                                   \
-      RA_READ_A(((kt_) + 1) % S, 0, fa0);                                                             \
-      RA_READ_B(((kt_) + 1) % S, FBN);                                                                \
-    }                                                                                                 \
-    RA_MMA(3, fa1, FBC);                                                                              \
-  }
+    const int sn_ = ((kt_) + 1) % S;                                                                \
+    RA_READ_A(sn_, 0, fa[0]);                                                                       \
+    RA_READ_B(sn_, 0, fbr[0]);                                                                      \
+  }                                                                                                 \
+  __builtin_amdgcn_sched_barrier(0);                                                                \
+  RA_MMA(fa[1], bq[1]);                                                                             \
+  RA_DEQ(0, fbr[0], bq[0]);                                                                         \
+  RA_INTERLEAVE_LATE();
 
   const int KT = K / BK;
 #pragma unroll
   for (int s = 0; s < S; ++s)
     if (s < KT) RA_ISSUE(s, s);
+  wait_tiles<COPIES>(min(KT, S) - 1);
+  asm volatile("s_barrier" ::: "memory");
+  RA_READ_A(0, 0, fa[0]);
+  RA_READ_B(0, 0, fbr[0]);
+  RA_DEQ(0, fbr[0], bq[0]);
+  int kt = 0;
+  // Steady state: tile kt+S exists, S-2 younger tiles in flight at the wait.
+  for (; kt < KT - S; ++kt) {
+    const int st = kt % S;
+    RA_SUBSTEPS_012(st);
+    RA_BOUNDARY_SUBSTEP3(kt, st, S - 2, true);
+  }
+  // Drain: no more copies to issue.
+  for (; kt < KT - 1; ++kt) {
+    const int st = kt % S;
+    RA_SUBSTEPS_012(st);
+    RA_BOUNDARY_SUBSTEP3(kt, st, KT - 2 - kt, false);
+  }
+  // Last tile.
   {
-    const int younger0 = min(KT, S) - 1;  // tiles issued after tile 0
-    if (younger0 >= 3) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * COPIES) : "memory");
-    else if (younger0 == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * COPIES) : "memory");
-    else if (younger0 == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(COPIES) : "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    asm volatile("s_barrier" ::: "memory");
+    const int st = kt % S;
+    RA_SUBSTEPS_012(st);
+    __builtin_amdgcn_sched_barrier(0);
+    RA_MMA(fa[1], bq[1]);
   }
-  RA_READ_A(0, 0, fa0);
-  RA_READ_B(0, fbA);
-  for (int kt = 0; kt < KT; kt += 2) {
-    RA_TILE(kt, fbA, fbB);
-    if (kt + 1 < KT) RA_TILE(kt + 1, fbB, fbA);
-  }
-#undef RA_TILE
+#undef RA_BOUNDARY_SUBSTEP3
+#undef RA_SUBSTEPS_012
+#undef RA_INTERLEAVE_LATE
+#undef RA_INTERLEAVE
+#undef RA_DEQ
 #undef RA_MMA
 #undef RA_READ_B
 #undef RA_READ_A
 #undef RA_ISSUE
 
-  // ---- epilogue (as tiled_kernel) ----
+  // ---- epilogue: scale (+ bias) or the gate/up SwiGLU on the fp32 sums ----
   if (GU) {
-    const int j = n0 + wn * 32 + l32;
-    if (j < N) {
+#pragma unroll
+    for (int bj = 0; bj < BNB / 2; ++bj) {
+      const int j = n0 + wn * (WN / 2) + bj * 32 + l32;
+      if (j >= N) continue;
       const float sg = scale[j], su = scale[N + j];
 #pragma unroll
-      for (int bi = 0; bi < 4; ++bi)
+      for (int bi = 0; bi < BMB; ++bi)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int m = m0 + wm * 128 + bi * 32 + (e & 3) + 8 * (e >> 2) + 4 * g;
-          if (m < M) y[(int64_t)m * ldy + j] = swiglu_out<Ac>(acc[bi][0][e] * sg, acc[bi][1][e] * su);
+          const int m = m0 + wm * WM + bi * 32 + (e & 3) + 8 * (e >> 2) + 4 * g;
+          if (m < M)
+            y[(int64_t)m * ldy + j] = swiglu_out<Ac>(acc[bi][bj][e] * sg, acc[bi][bj + BNB / 2][e] * su);
         }
     }
   } else {
 #pragma unroll
-    for (int bj = 0; bj < 2; ++bj) {
-      const int n = n0 + wn * 64 + bj * 32 + l32;
+    for (int bj = 0; bj < BNB; ++bj) {
+      const int n = n0 + wn * WN + bj * 32 + l32;
       if (n >= N) continue;
       const float sn = scale[n];
       const float bn = bias ? load_as_f32(bias, n, bias_dt) : 0.f;
 #pragma unroll
-      for (int bi = 0; bi < 4; ++bi)
+      for (int bi = 0; bi < BMB; ++bi)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int m = m0 + wm * 128 + bi * 32 + (e & 3) + 8 * (e >> 2) + 4 * g;
+          const int m = m0 + wm * WM + bi * 32 + (e & 3) + 8 * (e >> 2) + 4 * g;
           if (m < M) y[(int64_t)m * ldy + n] = Ac::out(acc[bi][bj][e] * sn + bn);
         }
     }
@@ -472,32 +553,95 @@ static bool tiled_shape_ok(int x_dt, const void *x, int64_t ldx, const int8_t *w
 
 bool tiled_supported(const GemmArgs &a) { return tiled_shape_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.M, a.N, a.K); }
 
+template <int DT, bool GU, int BMB, int BNB>
+static void launch_dma(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
+                       const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                       hipStream_t s) {
+  using G = DmaTile<BMB, BNB>;
+  constexpr int OUTN = GU ? G::BN / 2 : G::BN;
+  const int tiles_m = (int)((M + G::BM - 1) / G::BM);
+  const int tiles_n = (int)((N + OUTN - 1) / OUTN);
+  hipLaunchKernelGGL((tiled_dma_kernel<DT, GU, BMB, BNB>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s,
+                     static_cast<const uint16_t *>(x), ldx, w, ldw, scale, bias, bias_dt,
+                     static_cast<uint16_t *>(y), ldy, (int)M, (int)N, (int)K, tiles_m, tiles_n);
+}
+
+// Direct-to-LDS tile shapes, (BMB, BNB) = per-wave 32x32 blocks, and a
+// relative cost per output element of a full tile, measured on MI355X with
+// whole rounds of tiles (M=8192 K=4096 N=4096 and the 70B MLP shapes): (4,4)
+// reaches ~1130 TFLOP/s, (4,3) ~1025, (3,4) ~995, (4,2) ~885.
+struct DmaShape {
+  int bmb, bnb;
+  double cost;
+};
+constexpr DmaShape kDmaShapes[] = {{4, 4, 1.00}, {4, 3, 1.10}, {3, 4, 1.13}, {4, 2, 1.28}};
+
+// One workgroup per CU (160 KB LDS), so tiles run in rounds of `cus`; pick
+// the shape with the least (rounds x tile area x cost).
+static DmaShape pick_dma_shape(int64_t M, int64_t N, bool gu, int cus) {
+  DmaShape best = kDmaShapes[3];
+  double best_t = 0;
+  bool first = true;
+  for (const DmaShape &c : kDmaShapes) {
+    if (gu && c.bnb % 2) continue;
+    const int64_t bm = 64 * c.bmb, bn = 64 * c.bnb, outn = gu ? bn / 2 : bn;
+    const int64_t tiles = ((M + bm - 1) / bm) * ((N + outn - 1) / outn);
+    const int64_t rounds = (tiles + cus - 1) / cus;
+    const double t = (double)rounds * (double)(bm * bn) * c.cost;
+    if (first || t < best_t) best = c, best_t = t, first = false;
+  }
+  return best;
+}
+
+static int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
+template <int DT, bool GU>
+static void launch_dma_auto(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
+                            const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                            hipStream_t s, int forced) {
+  DmaShape c = pick_dma_shape(M, N, GU, device_cus());
+  if (forced == 3) c = {4, 2, 0};
+  if (forced == 4) c = {3, 4, 0};
+  if (forced == 5) c = {4, 4, 0};
+  if (forced == 6 && !GU) c = {4, 3, 0};
+  if (c.bmb == 4 && c.bnb == 4) return launch_dma<DT, GU, 4, 4>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  if (c.bmb == 3 && c.bnb == 4) return launch_dma<DT, GU, 3, 4>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  if constexpr (!GU) {
+    if (c.bmb == 4 && c.bnb == 3)
+      return launch_dma<DT, GU, 4, 3>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  }
+  launch_dma<DT, GU, 4, 2>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+}
+
 template <bool GU>
 static hipError_t launch(const void *x, int64_t ldx, int x_dt, const int8_t *w, int64_t ldw,
                          const float *scale, const void *bias, int bias_dt, void *y, int64_t ldy,
                          int64_t M, int64_t N, int64_t K, hipStream_t s) {
-  constexpr int OUTN = GU ? tiled::BN / 2 : tiled::BN;
-  const int tiles_m = (int)((M + tiled::BM - 1) / tiled::BM);
-  const int tiles_n = (int)((N + OUTN - 1) / OUTN);
-  const dim3 grid((unsigned)(tiles_m * tiles_n));
+  int forced = 0;
 #ifdef RA_TUNING
-  extern int g_tiled_mode;  // 0 auto, 1 register-staged kernel, 2 direct-to-LDS kernel
-  const bool use_dma = g_tiled_mode == 2 || (g_tiled_mode == 0 && K % tiled::BK == 0);
+  extern int g_tiled_mode;  // 0 auto, 1 register-staged kernel, 2 direct-to-LDS auto, 3.. forced shapes
+  forced = g_tiled_mode;
+  const bool use_dma = g_tiled_mode >= 2 || (g_tiled_mode == 0 && K % tiled::BK == 0);
 #else
   const bool use_dma = K % tiled::BK == 0;
 #endif
   if (use_dma) {
-    constexpr int S = RA_TILED_STAGES;
     if (x_dt == RA_F16)
-      hipLaunchKernelGGL((tiled_dma_kernel<RA_F16, GU, S>), grid, dim3(256), 0, s,
-                         static_cast<const uint16_t *>(x), ldx, w, ldw, scale, bias, bias_dt,
-                         static_cast<uint16_t *>(y), ldy, (int)M, (int)N, (int)K, tiles_m, tiles_n);
+      launch_dma_auto<RA_F16, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s, forced);
     else
-      hipLaunchKernelGGL((tiled_dma_kernel<RA_BF16, GU, S>), grid, dim3(256), 0, s,
-                         static_cast<const uint16_t *>(x), ldx, w, ldw, scale, bias, bias_dt,
-                         static_cast<uint16_t *>(y), ldy, (int)M, (int)N, (int)K, tiles_m, tiles_n);
+      launch_dma_auto<RA_BF16, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s, forced);
     return hipGetLastError();
   }
+  constexpr int OUTN = GU ? tiled::BN / 2 : tiled::BN;
+  const int tiles_m = (int)((M + tiled::BM - 1) / tiled::BM);
+  const int tiles_n = (int)((N + OUTN - 1) / OUTN);
+  const dim3 grid((unsigned)(tiles_m * tiles_n));
   if (x_dt == RA_F16)
     hipLaunchKernelGGL((tiled_kernel<RA_F16, GU>), grid, dim3(256), 0, s, static_cast<const uint16_t *>(x), ldx,
                        w, ldw, scale, bias, bias_dt, static_cast<uint16_t *>(y), ldy, (int)M, (int)N, (int)K,

@@ -179,6 +179,18 @@ def test_prefill_full_size(gpu, M, K, N, seed):
     _full_size_check(gemm_case(M, K, N, seed, device=gpu), gpu)
 
 
+# Shapes for which the tiled kernel picks each of its tile geometries
+# (per-wave 32x32 blocks (4,2), (4,3), (3,4), (4,4); one workgroup per CU on
+# 256 CUs), with M and N tails; short K keeps them fast.
+TILE_SHAPES = [(300, 192, 4096), (576, 256, 11264), (640, 128, 16384), (832, 128, 13312), (1000, 320, 13000)]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K,N", TILE_SHAPES)
+def test_tiled_tile_geometries(gpu, M, K, N, dt):
+    _full_size_check(gemm_case(M, K, N, seed=M + N, device=gpu, dtype=dt), gpu)
+
+
 @pytest.mark.parametrize("M", [1, 16, 2048])
 def test_deterministic(gpu, M):
     c = gemm_case(M, 4096, 4096, seed=21, device=gpu)

@@ -105,7 +105,7 @@ def _swiglu_chain64(g64, u64, dt):
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M,K,inter", [(1, 1024, 512), (5, 512, 300), (17, 2048, 640), (64, 256, 128),
-                                        (100, 512, 96), (300, 1024, 200)])
+                                        (100, 512, 96), (300, 1024, 200), (320, 128, 8704), (450, 128, 11264)])
 def test_gateup_swiglu_vs_oracle(gpu, dt, M, K, inter):
     g = torch.Generator().manual_seed(M + K)
     x = torch.randn(M, K, generator=g).to(dt)
