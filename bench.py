@@ -47,7 +47,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=3000)
     p.add_argument("--warmup", type=int, default=100)
-    p.add_argument("--prefill-steps", type=int, default=60)
+    p.add_argument("--prefill-steps", type=int, default=300)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--only", choices=("all", "decode", "prefill"), default="all",
@@ -129,9 +129,11 @@ def time_eager(launcher, steps: int, warmup: int):
     return start.elapsed_time(end) / steps
 
 
-def time_graph(launcher, steps: int, warmup: int, per_graph: int):
+def time_graph(launcher, steps: int, warmup: int, per_graph: int, warm_seconds: float = 0.2):
     """The same launches captured into one HIP graph of ``per_graph`` steps
     and replayed; HIP events on the launch stream bracket the timed replays.
+    Untimed replays run for at least ``warmup`` steps and ``warm_seconds``
+    first, so that the timed region starts at steady clocks.
     Returns (ms per step, steps actually timed)."""
     import torch
     side = torch.cuda.Stream()
@@ -144,8 +146,11 @@ def time_graph(launcher, steps: int, warmup: int, per_graph: int):
     with torch.cuda.graph(graph):
         launcher.run(per_graph)
     reps = max(1, -(-steps // per_graph))
-    for _ in range(max(1, -(-warmup // per_graph))):
+    t0, done = time.perf_counter(), 0
+    while done < warmup or time.perf_counter() - t0 < warm_seconds:
         graph.replay()
+        torch.cuda.synchronize()
+        done += per_graph
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()

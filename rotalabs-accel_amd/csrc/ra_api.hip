@@ -21,6 +21,7 @@ SkinnyCfg g_skinny_override{0, 0, 0};
 namespace ra {
 int g_tiled_mode = 0;
 int g_rows_rw = 0;
+int g_rows_pipe = 0;
 }
 #endif
 
@@ -67,6 +68,7 @@ extern "C" {
 void ra_tune_skinny(int mt, int rt, int nw) { g_skinny_override = SkinnyCfg{mt, rt, nw}; }
 void ra_tune_tiled(int mode) { ra::g_tiled_mode = mode; }
 void ra_tune_rows(int rw) { ra::g_rows_rw = rw; }
+void ra_tune_rows_pipe(int rp) { ra::g_rows_pipe = rp; }
 #endif
 
 int ra_abi_version(void) { return RA_ABI_VERSION; }

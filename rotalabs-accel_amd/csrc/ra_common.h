@@ -145,6 +145,23 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Wave64 sum through DPP lane moves (VALU only, no LDS round trips): quad
+// butterflies, half-row and row mirrors, then the row_bcast15 / row_bcast31
+// carries; the total ends in lane 63 and is returned to every lane.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_moved(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_moved<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v += dpp_moved<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v += dpp_moved<0x141, 0xF>(v);  // row_half_mirror
+  v += dpp_moved<0x140, 0xF>(v);  // row_mirror
+  v += dpp_moved<0x142, 0xA>(v);  // row_bcast15 into rows 1 and 3
+  v += dpp_moved<0x143, 0xC>(v);  // row_bcast31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));

@@ -89,6 +89,23 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t *__restri
   const uint16_t *xr[MR];
 #pragma unroll
   for (int m = 0; m < MR; ++m) xr[m] = x + (int64_t)(m < M ? m : 0) * ldx + 16 * lane;
+  // Epilogue operands are loaded up front, in flight with the weights (a load
+  // after the reduction would add a memory round trip to every wave).
+  // The bias is kept as raw bits until the end so that no conversion (and no
+  // wait) sits in front of the weight loads.
+  float sc[RW], su[RW];
+  uint32_t bb[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int n = min(n0 + r, N - 1);
+    sc[r] = scale[n];
+    su[r] = GU ? scale[N + n] : 0.f;
+    bb[r] = 0;
+    if (!GU && bias) {
+      if (bias_dt == RA_F32) bb[r] = static_cast<const uint32_t *>(bias)[n];
+      else bb[r] = static_cast<const uint16_t *>(bias)[n];
+    }
+  }
 
   float acc[NR][MR];
 #pragma unroll
@@ -146,20 +163,129 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t *__restri
       for (int m = 0; m < MR; ++m) acc[t][m] = dot16<DT>(wv[t], xa[m], xb[m], acc[t][m]);
   }
 
-  // Reduce over the wave; lane r stores row n0 + r.
+  // Reduce over the wave (DPP); lane r stores row n0 + r. Same arithmetic as
+  // epilogue_value: acc * scale, + bias only when there is one.
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
-      const float s0 = wave_sum(acc[r][m]);
-      const float s1 = GU ? wave_sum(acc[NR - RW + r][m]) : 0.f;
+      const float s0 = wave_sum_dpp(acc[r][m]);
+      const float s1 = GU ? wave_sum_dpp(acc[NR - RW + r][m]) : 0.f;
       const int n = n0 + r;
       if (lane == r && m < M && n < N) {
         uint16_t *yrow = y + (int64_t)m * ldy;
-        if (GU)
-          yrow[n] = swiglu_out<A>(s0 * scale[n], s1 * scale[N + n]);
-        else
-          yrow[n] = A::out(epilogue_value(s0, scale, bias, bias_dt, n));
+        if (GU) {
+          yrow[n] = swiglu_out<A>(s0 * sc[r], s1 * su[r]);
+        } else {
+          float v = s0 * sc[r];
+          if (bias)
+            v += bias_dt == RA_F32 ? __uint_as_float(bb[r])
+                                   : (bias_dt == RA_F16 ? f16_to_f32((uint16_t)bb[r]) : bf16_to_f32((uint16_t)bb[r]));
+          yrow[n] = A::out(v);
+        }
+      }
+    }
+  }
+}
+
+// Short-K variant (K <= 4096, one step): a wave handles RP consecutive rows
+// one after another, loading row r+1 while it reduces row r, so the wave's
+// 4 KB of weight loads stay in flight during the dot products; x[0:M, 0:K] is
+// loaded once per wave and kept in registers for all RP rows.
+template <int DT, int MR, int RP, bool GU>
+__global__ __launch_bounds__(256) void gemv_rows_pipe_kernel(const uint16_t *__restrict__ x, int64_t ldx,
+                                                             const int8_t *__restrict__ w, int64_t ldw,
+                                                             const float *__restrict__ scale,
+                                                             const void *__restrict__ bias, int bias_dt,
+                                                             uint16_t *__restrict__ y, int64_t ldy, int M,
+                                                             int N, int K) {
+  using A = Act<DT>;
+  constexpr int NT = GU ? 2 : 1;  // weight rows per output row: gate (and up)
+  const int lane = threadIdx.x & 63;
+  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RP;
+  if (n0 >= N) return;  // whole wave; no barriers in this kernel
+  // Window c covers k = 1024c + 16*lane .. +15; lanes past K re-read the first
+  // 16 elements of the row (offset 0 from the row start; K >= 16) and
+  // contribute zeros.
+  int off[kRowsCh];
+  bool ok[kRowsCh];
+#pragma unroll
+  for (int c = 0; c < kRowsCh; ++c) {
+    ok[c] = 1024 * c + 16 * lane + 16 <= K;
+    off[c] = ok[c] ? 1024 * c + 16 * lane : 0;
+  }
+  uint4 wv[2][kRowsCh][NT];
+  auto load_row = [&](int r, uint4(&dst)[kRowsCh][NT]) {
+    const int n = min(n0 + r, N - 1);  // rows past N: in bounds, never stored
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int8_t *row = w + (int64_t)(t ? N + n : n) * ldw;
+#pragma unroll
+      for (int c = 0; c < kRowsCh; ++c) dst[c][t] = *reinterpret_cast<const uint4 *>(row + off[c]);
+    }
+  };
+  load_row(0, wv[0]);
+  uint4 xa[kRowsCh][MR], xb[kRowsCh][MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    const uint16_t *xrow = x + (int64_t)(m < M ? m : 0) * ldx;  // rows m >= M alias row 0, never stored
+#pragma unroll
+    for (int c = 0; c < kRowsCh; ++c) {
+      xa[c][m] = *reinterpret_cast<const uint4 *>(xrow + off[c]);
+      xb[c][m] = *reinterpret_cast<const uint4 *>(xrow + off[c] + 8);
+    }
+  }
+  float sc[RP], su[RP];
+  uint32_t bb[RP];
+#pragma unroll
+  for (int r = 0; r < RP; ++r) {
+    const int n = min(n0 + r, N - 1);
+    sc[r] = scale[n];
+    su[r] = GU ? scale[N + n] : 0.f;
+    bb[r] = 0;
+    if (!GU && bias) {
+      if (bias_dt == RA_F32) bb[r] = static_cast<const uint32_t *>(bias)[n];
+      else bb[r] = static_cast<const uint16_t *>(bias)[n];
+    }
+  }
+  // Operands of windows past K are replaced by zeros at use (selects into new
+  // registers: overwriting a register with a load in flight would wait).
+  const uint4 z = make_uint4(0, 0, 0, 0);
+
+#pragma unroll
+  for (int r = 0; r < RP; ++r) {
+    if (r + 1 < RP) load_row(r + 1, wv[(r + 1) & 1]);
+    __builtin_amdgcn_sched_barrier(0);  // next row's loads go out before this row's wait
+    float acc[NT][MR];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) acc[t][m] = 0.f;
+#pragma unroll
+    for (int c = 0; c < kRowsCh; ++c)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const uint4 wc = ok[c] ? wv[r & 1][c][t] : z;
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+          acc[t][m] = dot16<DT>(wc, ok[c] ? xa[c][m] : z, ok[c] ? xb[c][m] : z, acc[t][m]);
+      }
+    const int n = n0 + r;
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float s0 = wave_sum_dpp(acc[0][m]);
+      const float s1 = GU ? wave_sum_dpp(acc[NT - 1][m]) : 0.f;
+      if (lane == 0 && m < M && n < N) {
+        uint16_t *yrow = y + (int64_t)m * ldy;
+        if (GU) {
+          yrow[n] = swiglu_out<A>(s0 * sc[r], s1 * su[r]);
+        } else {
+          float v = s0 * sc[r];
+          if (bias)
+            v += bias_dt == RA_F32 ? __uint_as_float(bb[r])
+                                   : (bias_dt == RA_F16 ? f16_to_f32((uint16_t)bb[r]) : bf16_to_f32((uint16_t)bb[r]));
+          yrow[n] = A::out(v);
+        }
       }
     }
   }
@@ -224,12 +350,55 @@ static void rows_go_rw(const RowsParams &p, int rw, hipStream_t s) {
   rows_go<DT, MR, 1, GU>(p, s);
 }
 
+// Rows per wave of the short-K variant (used for M == 2, where a wave's dot
+// products take long enough to be worth overlapping with the next row's
+// loads; at M == 1 it measured the same as one row per wave): up to 4 rows
+// while >= 2048 waves remain.
+static int rows_pipe_rows(int64_t M, int64_t N, int64_t K, bool gu) {
+  int rp = 0;
+  if (M == 2 && K <= 1024 * kRowsCh) {
+    rp = 4;
+    while (rp > 1 && N / rp < 2048) rp >>= 1;
+  }
+#ifdef RA_TUNING
+  extern int g_rows_pipe;  // 0 auto, -1 off, else forced rows per wave
+  if (g_rows_pipe == -1) rp = 0;
+  else if (g_rows_pipe > 0 && K <= 1024 * kRowsCh) rp = g_rows_pipe;
+#endif
+  return rp;
+}
+
+template <int DT, int MR, bool GU>
+static void rows_pipe_go(const RowsParams &p, int rp, hipStream_t s) {
+  const int64_t waves = ((int64_t)p.N + rp - 1) / rp;
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+#define RA_PIPE(RP_)                                                                                      \
+  hipLaunchKernelGGL((gemv_rows_pipe_kernel<DT, MR, RP_, GU>), grid, block, 0, s, p.x, p.ldx, p.w, p.ldw, \
+                     p.scale, p.bias, p.bias_dt, p.y, p.ldy, p.M, p.N, p.K)
+  if (rp >= 4) RA_PIPE(4);
+  else if (rp == 3) RA_PIPE(3);
+  else if (rp == 2) RA_PIPE(2);
+  else RA_PIPE(1);
+#undef RA_PIPE
+}
+
 template <bool GU>
 static hipError_t rows_launch(const void *x, int64_t ldx, int x_dt, const int8_t *w, int64_t ldw,
                               const float *scale, const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M,
                               int64_t N, int64_t K, hipStream_t s) {
   const RowsParams p{static_cast<const uint16_t *>(x), ldx, w, ldw, scale, bias, bias_dt,
                      static_cast<uint16_t *>(y), ldy, (int)M, (int)N, (int)K};
+  const int rp = rows_pipe_rows(M, N, K, GU);
+  if (rp > 0) {
+    if (x_dt == RA_F16) {
+      if (M == 1) rows_pipe_go<RA_F16, 1, GU>(p, rp, s);
+      else rows_pipe_go<RA_F16, 2, GU>(p, rp, s);
+    } else {
+      if (M == 1) rows_pipe_go<RA_BF16, 1, GU>(p, rp, s);
+      else rows_pipe_go<RA_BF16, 2, GU>(p, rp, s);
+    }
+    return hipGetLastError();
+  }
   const int rw = rows_per_wave(M, N, GU);
   if (x_dt == RA_F16) {
     if (M == 1) rows_go_rw<RA_F16, 1, GU>(p, rw, s);
