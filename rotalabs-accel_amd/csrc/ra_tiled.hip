@@ -33,6 +33,8 @@
 // GU (gate/up + SwiGLU): the 128 B rows of a tile are 64 gate rows and the
 // 64 matching up rows, arranged so that each wave's two 32-column blocks are
 // the gate and up values of the same 32 output columns.
+#include <type_traits>
+
 #include "ra_common.h"
 #include "ra_internal.h"
 
@@ -507,51 +509,84 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
 #undef RA_ISSUE
 
   // ---- epilogue: scale (+ bias) or the gate/up SwiGLU on the fp32 sums ----
-  if (GU) {
+  // Lane (l32, g) holds, for block (bi, bj), column l32 of rows
+  // 32*bi + r(e) + 4g, r(e) = (e & 3) + 8 * (e >> 2). The row offsets
+  // r(e) * ldy are uniform; the bias test and the row guard (only tiles that
+  // reach past M need it) are hoisted out of the store loops.
+  // Addresses: a uniform base (wave's first row and column) plus a 32-bit
+  // per-lane element offset (BM * ldy < 2^31 is checked on the host).
+  const int row_l = m0 + wm * WM + 4 * g;
+  const int rows_left = M - row_l;  // rows r < rows_left are in range
+  const int col_w = n0 + wn * (GU ? WN / 2 : WN);  // wave's first output column
+  uint16_t *const yw = y + (int64_t)(m0 + wm * WM) * ldy + col_w;
+  const uint32_t ldy32 = (uint32_t)ldy;
+  const uint32_t lane_off = 4u * (uint32_t)g * ldy32 + (uint32_t)l32;
+  auto store_blocks = [&](auto guard_c, auto bias_c) {
+    constexpr bool GUARD = decltype(guard_c)::value, HAS_BIAS = decltype(bias_c)::value;
+    if constexpr (GU) {
 #pragma unroll
-    for (int bj = 0; bj < BNB / 2; ++bj) {
-      const int j = n0 + wn * (WN / 2) + bj * 32 + l32;
-      if (j >= N) continue;
-      const float sg = scale[j], su = scale[N + j];
+      for (int bj = 0; bj < BNB / 2; ++bj) {
+        const int j = n0 + wn * (WN / 2) + bj * 32 + l32;
+        if (j >= N) continue;
+        const float sg = scale[j], su = scale[N + j];
 #pragma unroll
-      for (int bi = 0; bi < BMB; ++bi)
+        for (int bi = 0; bi < BMB; ++bi)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int m = m0 + wm * WM + bi * 32 + (e & 3) + 8 * (e >> 2) + 4 * g;
-          if (m < M)
-            y[(int64_t)m * ldy + j] = swiglu_out<Ac>(acc[bi][bj][e] * sg, acc[bi][bj + BNB / 2][e] * su);
-        }
+          for (int e = 0; e < 16; ++e) {
+            const int r = bi * 32 + (e & 3) + 8 * (e >> 2);
+            if (!GUARD || r < rows_left)
+              yw[lane_off + (uint32_t)r * ldy32 + 32u * bj] =
+                  swiglu_out<Ac>(acc[bi][bj][e] * sg, acc[bi][bj + BNB / 2][e] * su);
+          }
+      }
+    } else {
+#pragma unroll
+      for (int bj = 0; bj < BNB; ++bj) {
+        const int n = n0 + wn * WN + bj * 32 + l32;
+        if (n >= N) continue;
+        const float sn = scale[n];
+        const float bn = HAS_BIAS ? load_as_f32(bias, n, bias_dt) : 0.f;
+#pragma unroll
+        for (int bi = 0; bi < BMB; ++bi)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int r = bi * 32 + (e & 3) + 8 * (e >> 2);
+            if (!GUARD || r < rows_left) {
+              float v = acc[bi][bj][e] * sn;
+              if (HAS_BIAS) v += bn;
+              yw[lane_off + (uint32_t)r * ldy32 + 32u * bj] = Ac::out(v);
+            }
+          }
+      }
     }
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  const bool guard = m0 + BM > M;
+  if (bias) {
+    if (guard) store_blocks(T_{}, T_{});
+    else store_blocks(F_{}, T_{});
   } else {
-#pragma unroll
-    for (int bj = 0; bj < BNB; ++bj) {
-      const int n = n0 + wn * WN + bj * 32 + l32;
-      if (n >= N) continue;
-      const float sn = scale[n];
-      const float bn = bias ? load_as_f32(bias, n, bias_dt) : 0.f;
-#pragma unroll
-      for (int bi = 0; bi < BMB; ++bi)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int m = m0 + wm * WM + bi * 32 + (e & 3) + 8 * (e >> 2) + 4 * g;
-          if (m < M) y[(int64_t)m * ldy + n] = Ac::out(acc[bi][bj][e] * sn + bn);
-        }
-    }
+    if (guard) store_blocks(T_{}, F_{});
+    else store_blocks(F_{}, F_{});
   }
 }
 
-static bool tiled_shape_ok(int x_dt, const void *x, int64_t ldx, const int8_t *w, int64_t ldw, int64_t M,
-                           int64_t N, int64_t K) {
+static bool tiled_shape_ok(int x_dt, const void *x, int64_t ldx, const int8_t *w, int64_t ldw, int64_t ldy,
+                           int64_t M, int64_t N, int64_t K) {
   if (x_dt != RA_F16 && x_dt != RA_BF16) return false;
   if (M > ((int64_t)1 << 30) || N > ((int64_t)1 << 30) || K > ((int64_t)1 << 30)) return false;
   if (K % 16 != 0) return false;
   if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w) & 15)) return false;
   if ((ldx % 8) != 0 || (ldw % 16) != 0) return false;
+  if (ldy > ((int64_t)1 << 22)) return false;  // 32-bit epilogue offsets: 256 * ldy < 2^31
   const int64_t tiles = ((M + tiled::BM - 1) / tiled::BM) * ((N + tiled::BN - 1) / tiled::BN);
   return tiles < ((int64_t)1 << 31);
 }
 
-bool tiled_supported(const GemmArgs &a) { return tiled_shape_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.M, a.N, a.K); }
+bool tiled_supported(const GemmArgs &a) {
+  return tiled_shape_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.ldy, a.M, a.N, a.K);
+}
 
 template <int DT, bool GU, int BMB, int BNB>
 static void launch_dma(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
@@ -659,7 +694,7 @@ hipError_t tiled_launch(const GemmArgs &a, hipStream_t s) {
 }
 
 bool gateup_tiled_supported(const GateUpArgs &a) {
-  return tiled_shape_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.M, 2 * a.I, a.K);
+  return tiled_shape_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.ldh, a.M, 2 * a.I, a.K);
 }
 
 hipError_t gateup_tiled_launch(const GateUpArgs &a, hipStream_t s) {
