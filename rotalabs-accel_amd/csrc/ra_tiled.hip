@@ -247,11 +247,19 @@ __device__ __forceinline__ uint32_t lds_offset(const void *p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
-// 16 bytes per lane from global memory to LDS at m0 + 16 * lane. An LDS DMA
-// that reads M0 needs one wait state after the SALU write of M0.
-__device__ __forceinline__ void dma16(const void *g, uint32_t lds_wave_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_wave_base), "v"(g)
-               : "memory", "m0");
+// 16 bytes per lane from global memory to LDS at M0 + OFS + 16 * lane; the
+// instruction offset OFS is added to both the global and the LDS address, so
+// up to four consecutive 1 KB copies share one M0 value (the caller passes
+// g - OFS). NEW_M0 first writes M0; an LDS DMA that reads M0 needs one wait
+// state after that SALU write.
+template <int OFS, bool NEW_M0>
+__device__ __forceinline__ void dma16(const void *g_minus_ofs, uint32_t m0_value) {
+  if (NEW_M0)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off offset:%2" ::"s"(m0_value),
+                 "v"(g_minus_ofs), "n"(OFS)
+                 : "memory", "m0");
+  else
+    asm volatile("global_load_lds_dwordx4 %0, off offset:%1" ::"v"(g_minus_ofs), "n"(OFS) : "memory");
 }
 
 // Tile geometry of the direct-to-LDS kernel: 4 waves in a 2 x 2 grid, each
@@ -273,6 +281,15 @@ struct DmaTile {
   static_assert(S >= 2 && S <= 4, "2 to 4 stages");
   static_assert((S - 1) * COPIES <= 63, "vmcnt is a 6-bit counter");
 };
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [LO, HI).
+template <int LO, int HI, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (LO < HI) {
+    f(std::integral_constant<int, LO>{});
+    static_for<LO + 1, HI>(f);
+  }
+}
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -336,7 +353,7 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
     const int c = (lane & 7) ^ ((row >> 1) & 7);
     int gr = m0 + row;
     gr = gr < M ? gr : M - 1;
-    a_src[i] = x + (int64_t)gr * ldx + c * 8;
+    a_src[i] = x + (int64_t)gr * ldx + c * 8 - (i % 4) * 512;  // - instruction offset (bytes / 2)
   }
   // B copy i covers tile rows 16*bi .. +15 (bi = B_COPIES*wid + i), lane ->
   // row 16*bi + lane/4, LDS chunk lane%4 <- global chunk (lane%4)^((row>>2)&3).
@@ -355,7 +372,7 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
       wr = n0 + row;
       wr = wr < N ? wr : N - 1;
     }
-    b_src[i] = w + (int64_t)wr * ldw + c * 16;
+    b_src[i] = w + (int64_t)wr * ldw + c * 16 - (i % 4) * 1024;  // - instruction offset
   }
   const uint32_t lds0 = lds_offset(lds);
   const uint32_t a_dst = lds0 + (uint32_t)(A_COPIES * wid) * 1024;
@@ -363,16 +380,25 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
 
 // Copies [LO_, HI_) of K tile kt_ into stage st_ (copies 0..A_COPIES-1 are
 // the A copies, the rest the B copies).
+// A copy's local index li (within A or B) selects M0 group li/4 and
+// instruction offset (li%4)*1024; the copy sources are stored pre-adjusted by
+// -(li%4)*1024 bytes. M0 is written at the first copy of a part and of each
+// group.
 #define RA_ISSUE_PART(kt_, st_, LO_, HI_)                                                   \
   {                                                                                         \
     const int kofs_ = (kt_) * BK;                                                           \
     const uint32_t so_ = (uint32_t)(st_) * STAGE;                                           \
-    _Pragma("unroll") for (int i = (LO_); i < (HI_); ++i) {                                 \
-      if (i < A_COPIES)                                                                     \
-        dma16(a_src[i] + kofs_, a_dst + so_ + (uint32_t)i * 1024);                         \
+    static_for<LO_, HI_>([&](auto ic_) {                                                    \
+      constexpr int i = decltype(ic_)::value;                                               \
+      constexpr bool isA = i < A_COPIES;                                                    \
+      constexpr int li = isA ? i : i - A_COPIES;                                            \
+      constexpr bool fresh = i == (LO_) || i == A_COPIES || li % 4 == 0;                    \
+      const uint32_t m0v = (isA ? a_dst : b_dst) + so_ + (uint32_t)(li / 4) * 4096;         \
+      if constexpr (isA)                                                                    \
+        dma16<(li % 4) * 1024, fresh>(a_src[li] + kofs_, m0v);                              \
       else                                                                                  \
-        dma16(b_src[i - A_COPIES] + kofs_, b_dst + so_ + (uint32_t)(i - A_COPIES) * 1024); \
-    }                                                                                       \
+        dma16<(li % 4) * 1024, fresh>(b_src[li] + kofs_, m0v);                              \
+    });                                                                                     \
   }
 #define RA_ISSUE(kt_, st_) RA_ISSUE_PART(kt_, st_, 0, COPIES)
 // In the steady state a tile's copies are spread over the first three
