@@ -13,6 +13,9 @@ Metric: int8_gemm HBM GB/s at M=1 and TFLOP/s at M=2048 (K=4096, N=11008).
 * ``roofline``: the dominant kernel's achieved GB/s (TFLOP/s for prefill)
   from HIP events on the launch stream, against MI355X peaks (HBM 8 TB/s,
   dense fp16 MFMA 2516.6 TFLOP/s).
+* ``mlp``: the fused decoder MLP block (RMSNorm -> int8 gate/up + SwiGLU ->
+  int8 down, bf16, H=8192, I=28672) per call at M=1 (GB/s) and M=4096
+  (TFLOP/s), graph replay.
 * ``cpu_baseline``: the reference's CPU fallback (dequantize + F.linear per
   call), restated in oracle/, timed on this host on a bounded sample.
 
@@ -50,8 +53,9 @@ def parse():
     p.add_argument("--prefill-steps", type=int, default=300)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", choices=("all", "decode", "prefill"), default="all",
+    p.add_argument("--only", choices=("all", "decode", "prefill", "mlp"), default="all",
                    help="run one workload only (for profiler runs)")
+    p.add_argument("--no-mlp", action="store_true", help="skip the fused-MLP timing")
     p.add_argument("--no-graph", action="store_true",
                    help="time host-launched loops instead of HIP graph replay (for counter runs)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -247,6 +251,44 @@ def run_prefill(args, dev):
     return pms, tflops, pvariant
 
 
+MLP = (8192, 28672)   # hidden, intermediate (70B-class decoder MLP, bf16)
+
+
+def run_mlp(args, dev):
+    """Fused decoder MLP block (RMSNorm -> gate/up + SwiGLU -> down, bf16,
+    H=8192, I=28672) at M=1 and M=4096, random int8 weights generated on the
+    GPU; returns a dict for the JSON line."""
+    import torch
+    import rotalabs_accel as ra
+    from rotalabs_accel.kernels.mlp import int8_mlp
+    from workloads import mlp_bytes, mlp_flops
+    H, I = MLP
+    g = torch.Generator(device=dev).manual_seed(11)
+    norm_w = (1.0 + 0.01 * torch.randn(H, device=dev, generator=g)).to(torch.bfloat16)
+    q_gu, s_gu = ra.quantize_weight_per_channel(torch.randn(2 * I, H, device=dev, generator=g) * 0.02)
+    q_d, s_d = ra.quantize_weight_per_channel(torch.randn(H, I, device=dev, generator=g) * 0.02)
+    out = {}
+    for M, calls in ((1, 20), (4096, 3)):
+        x = torch.randn(M, H, device=dev, generator=g).to(torch.bfloat16)
+
+        class _Step:
+            def run(self, n):
+                for _ in range(n):
+                    int8_mlp(x, norm_w, q_gu, s_gu, q_d, s_d)
+        ms, _ = time_graph(_Step(), calls * 3, calls, per_graph=calls)
+        rec = {"us_per_call": round(ms * 1e3, 2)}
+        if M == 1:
+            gbs = mlp_bytes(M, H, I) / (ms * 1e-3) / 1e9
+            rec.update({"GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)})
+        else:
+            tf = mlp_flops(M, H, I) / (ms * 1e-3) / 1e12
+            rec.update({"TFLOP/s": round(tf, 1), "frac_mfma": round(tf / PEAK_FP16_TFLOPS, 4)})
+        out[f"M={M}"] = rec
+        log(f"mlp M={M} H={H} I={I} bf16: {rec}")
+        del x
+    return out
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -285,6 +327,9 @@ def main():
     pvariant = None
     if args.only in ("all", "prefill"):
         pms, tflops, pvariant = run_prefill(args, dev)
+    mlp = None
+    if args.only == "mlp" or (args.only == "all" and not args.no_mlp):
+        mlp = run_mlp(args, dev)
     if args.only != "all":
         return
 
@@ -333,6 +378,9 @@ def main():
                                                      VARIANT_KERNELS.get(pvariant, ""))},
         },
     }
+    if mlp is not None:
+        out["mlp"] = {"workload": "fused decoder MLP (RMSNorm -> int8 gate/up + SwiGLU -> int8 down), bf16, "
+                                  "H=8192, I=28672, random int8 per-channel weights", **mlp}
     if cpu is not None:
         out["cpu_baseline"] = {
             "value": round(cpu["gbs"], 3), "unit": "GB/s", "cores": cpu["threads"], "kind": "port",

@@ -47,9 +47,83 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(const void *__rest
   }
 }
 
+// Same arithmetic for x, w, y of one 16-bit dtype with hidden % 8 == 0: every
+// thread loads its VPT 16-byte chunks of the row (and of w) at once, keeps them
+// in registers for the normalisation, and stores 16-byte chunks -- one pass
+// over memory with all loads in flight, instead of a latency-bound loop.
+template <int DT, int VPT>
+__global__ __launch_bounds__(kRowThreads) void rmsnorm_vec_kernel(const uint16_t *__restrict__ x, int64_t ldx,
+                                                                  const uint16_t *__restrict__ w,
+                                                                  uint16_t *__restrict__ y, int64_t ldy,
+                                                                  int hidden, float eps) {
+  using A = Act<DT>;
+  __shared__ float smem[kRowThreads / 64];
+  const int64_t row = blockIdx.x;
+  const int nch = hidden / 8;
+  const uint16_t *xr = x + row * ldx;
+  uint4 xv[VPT], wv[VPT];
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = min((int)threadIdx.x + kRowThreads * j, nch - 1);  // clamped: loads stay unconditional
+    xv[j] = *reinterpret_cast<const uint4 *>(xr + 8 * c);
+    wv[j] = *reinterpret_cast<const uint4 *>(w + 8 * c);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    if ((int)threadIdx.x + kRowThreads * j >= nch) continue;
+    const uint16_t *h = reinterpret_cast<const uint16_t *>(&xv[j]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = A::in(h[e]);
+      ss += v * v;
+    }
+  }
+  const float total = block_reduce<false>(ss, smem);
+  const float r = 1.0f / sqrtf(total / (float)hidden + eps);
+#pragma unroll
+  for (int j = 0; j < VPT; ++j) {
+    const int c = (int)threadIdx.x + kRowThreads * j;
+    if (c >= nch) continue;
+    const uint16_t *h = reinterpret_cast<const uint16_t *>(&xv[j]);
+    const uint16_t *hw = reinterpret_cast<const uint16_t *>(&wv[j]);
+    uint4 o;
+    uint16_t *ho = reinterpret_cast<uint16_t *>(&o);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ho[e] = A::out(A::rnd(A::in(h[e]) * r) * A::in(hw[e]));
+    *reinterpret_cast<uint4 *>(y + row * ldy + 8 * c) = o;
+  }
+}
+
+template <int DT>
+static void rmsnorm_vec_launch(const void *x, int64_t ldx, const void *w, void *y, int64_t ldy, int64_t rows,
+                               int hidden, float eps, hipStream_t s) {
+  const int nch = hidden / 8;
+  const uint16_t *xp = static_cast<const uint16_t *>(x), *wp = static_cast<const uint16_t *>(w);
+  uint16_t *yp = static_cast<uint16_t *>(y);
+  const dim3 grid((unsigned)rows), block(kRowThreads);
+  if (nch <= kRowThreads)
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 1>), grid, block, 0, s, xp, ldx, wp, yp, ldy, hidden, eps);
+  else if (nch <= 2 * kRowThreads)
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 2>), grid, block, 0, s, xp, ldx, wp, yp, ldy, hidden, eps);
+  else if (nch <= 4 * kRowThreads)
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 4>), grid, block, 0, s, xp, ldx, wp, yp, ldy, hidden, eps);
+  else
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 8>), grid, block, 0, s, xp, ldx, wp, yp, ldy, hidden, eps);
+}
+
 hipError_t rmsnorm_launch(const void *x, int64_t ldx, int x_dt, const void *w, int w_dt, void *y,
                           int64_t ldy, int y_dt, int64_t rows, int64_t hidden, float eps,
                           hipStream_t s) {
+  const bool vec = (x_dt == RA_F16 || x_dt == RA_BF16) && w_dt == x_dt && y_dt == x_dt && hidden % 8 == 0 &&
+                   hidden >= 8 && hidden <= 8 * 8 * kRowThreads && ldx % 8 == 0 && ldy % 8 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                     reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+  if (vec) {
+    if (x_dt == RA_F16) rmsnorm_vec_launch<RA_F16>(x, ldx, w, y, ldy, rows, (int)hidden, eps, s);
+    else rmsnorm_vec_launch<RA_BF16>(x, ldx, w, y, ldy, rows, (int)hidden, eps, s);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kRowThreads), 0, s, x, ldx, x_dt, w, w_dt,
                      y, ldy, y_dt, (int)hidden, eps);
   return hipGetLastError();

@@ -71,6 +71,19 @@ def test_rmsnorm_vs_oracle(gpu, xdt, wdt):
         assert (y == ref).float().mean() > 0.99
 
 
+@pytest.mark.parametrize("rows,hidden", [(1, 8200), (5, 40), (3, 16384), (2, 16392)])
+def test_rmsnorm_widths(gpu, rows, hidden):
+    """Row widths that leave threads idle, need several 16-byte chunks per
+    thread with a ragged tail, or exceed the single-pass kernel's width."""
+    g = torch.Generator().manual_seed(hidden)
+    x = (torch.randn(rows, hidden, generator=g) * 3).to(torch.bfloat16)
+    w = (1 + 0.01 * torch.randn(hidden, generator=g)).to(torch.bfloat16)
+    y = ra.rmsnorm(x.to(gpu), w.to(gpu), 1e-6).cpu()
+    ref = fallback.rmsnorm_ref(x, w, 1e-6)
+    torch.testing.assert_close(y.float(), ref.float(), rtol=1e-2, atol=1e-2)
+    assert (y == ref).float().mean() > 0.99
+
+
 def test_rmsnorm_golden(gpu, golden):
     x = _t16(golden["rms_x_bf16"], torch.bfloat16)
     w = _t16(golden["rms_w_bf16"], torch.bfloat16)
