@@ -45,7 +45,8 @@ enum ra_variant {
   RA_VARIANT_TILED = 2,   /* LDS-staged double-buffered MFMA GEMM (prefill)   */
   RA_VARIANT_GENERIC = 3, /* any shape / alignment / dtype, VALU, slow        */
   RA_VARIANT_GEMV = 4,    /* decode GEMV, M <= 4, x staged in LDS             */
-  RA_VARIANT_ROWS = 5     /* decode row GEMV, M <= 2, one weight row per wave */
+  RA_VARIANT_ROWS = 5,    /* decode row GEMV, M <= 2, one weight row per wave */
+  RA_VARIANT_BATCH = 6    /* small batch, M <= 64, K % 128 == 0, MFMA + LDS */
 };
 
 /* Version of this ABI (RA_ABI_VERSION of the built library). */

@@ -22,6 +22,7 @@ namespace ra {
 int g_tiled_mode = 0;
 int g_rows_rw = 0;
 int g_rows_pipe = 0;
+int g_batch_rt = 0;
 }
 #endif
 
@@ -42,8 +43,10 @@ constexpr int64_t kSkinnyMaxM = 64;
 int select_variant(const GemmArgs &a) {
   if (a.K == 0) return RA_VARIANT_GENERIC;
   if (gemv_rows_supported(a)) return RA_VARIANT_ROWS;
-  // M = 3..64: the split-K MFMA kernel measured faster than the LDS GEMV
-  // (M=4 K=4096 N=11008: 14.9 vs 17.8 us); the GEMV stays as a fallback.
+  // M = 3..64: the small-batch kernel (line-wide weight loads, activations
+  // read once per 48 rows) where K % 128 == 0, else the split-K MFMA kernel;
+  // both measured faster than the LDS GEMV, which stays as a fallback.
+  if (a.M <= kSkinnyMaxM && batch_supported(a)) return RA_VARIANT_BATCH;
   if (a.M <= kSkinnyMaxM && skinny_supported(a)) return RA_VARIANT_SKINNY;
   if (gemv_supported(a)) return RA_VARIANT_GEMV;
   if (tiled_supported(a)) return RA_VARIANT_TILED;
@@ -71,6 +74,7 @@ void ra_tune_skinny(int mt, int rt, int nw) { g_skinny_override = SkinnyCfg{mt, 
 void ra_tune_tiled(int mode) { ra::g_tiled_mode = mode; }
 void ra_tune_rows(int rw) { ra::g_rows_rw = rw; }
 void ra_tune_rows_pipe(int rp) { ra::g_rows_pipe = rp; }
+void ra_tune_batch_rt(int rt) { ra::g_batch_rt = rt; }
 #endif
 
 int ra_abi_version(void) { return RA_ABI_VERSION; }
@@ -106,6 +110,9 @@ int ra_w8a16_gemm_ex(const void *x, int64_t ldx, int x_dtype, const int8_t *w, i
     case RA_VARIANT_GEMV:
       if (!gemv_supported(a)) return RA_ERR_VARIANT;
       return to_status(gemv_launch(a, s));
+    case RA_VARIANT_BATCH:
+      if (!batch_supported(a)) return RA_ERR_VARIANT;
+      return to_status(batch_launch(a, s));
     case RA_VARIANT_TILED:
       if (!tiled_supported(a) || K == 0) return RA_ERR_VARIANT;
       return to_status(tiled_launch(a, s));
@@ -141,6 +148,7 @@ int ra_w8a16_gateup_swiglu(const void *x, int64_t ldx, int x_dtype, const int8_t
   const GateUpArgs a{x, ldx, x_dtype, w, ldw, scale, h, ldh, M, I, K};
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (K > 0 && gateup_gemv_rows_supported(a)) return to_status(gateup_gemv_rows_launch(a, s));
+  if (K > 0 && M <= kSkinnyMaxM && gateup_batch_supported(a)) return to_status(gateup_batch_launch(a, s));
   if (K > 0 && M <= kSkinnyMaxM && gateup_skinny_supported(a)) return to_status(gateup_skinny_launch(a, s));
   if (K > 0 && gateup_gemv_supported(a)) return to_status(gateup_gemv_launch(a, s));
   if (K > 0 && gateup_tiled_supported(a)) return to_status(gateup_tiled_launch(a, s));

@@ -1,0 +1,290 @@
+// Small-batch W8A16 GEMM (3 <= M <= 64) on gfx950.
+//
+// Replaces the reference's Triton tile loop (src/rotalabs_accel/kernels/
+// gemm.py:113-138) for small batches. Like the decode kernels the cost is the
+// weight stream (N*K bytes, 2*M flops per byte), but M is large enough that
+// the dot products belong on the matrix cores:
+//
+//  * Y^T = W . X^T with v_mfma_f32_16x16x32_{f16,bf16}: MFMA rows are weight
+//    rows, MFMA columns activation rows (M padded to 16*MT).
+//  * A workgroup owns 16*RT weight rows (32*RT with the gate/up pair); its NW
+//    waves split K into slices and combine their partial sums through LDS in a
+//    fixed order (deterministic, no workspace).
+//  * Weights are streamed in stages of 128 k: one stage of a wave's 16*NTW rows
+//    is loaded with 128-bit loads covering 8 rows x 128 contiguous bytes per
+//    wave instruction (full cache lines; the MFMA operand layout, 16 rows x 64
+//    bytes per instruction, streams HBM markedly slower), D stages in flight.
+//    Each stage is transposed through a wave-private LDS slot (16-byte chunks
+//    XOR-swizzled by (row >> 1) & 7, conflict-free both ways) into the MFMA
+//    layout, then dequantised exactly in registers.
+//  * Activation fragments are read from global memory (L2-resident) in the
+//    MFMA layout, in flight together with the stage's weights.
+//  * Scale (+ bias) or the gate/up SwiGLU is applied to the fp32 sums, one
+//    rounding.
+#include "ra_common.h"
+#include "ra_internal.h"
+
+namespace ra {
+
+namespace batch {
+constexpr int KS = 128;  // k per stage
+constexpr int kMaxM = 64;
+}  // namespace batch
+
+template <int DT, int MT, int RT, int NW, int D, bool GU>
+__global__ __launch_bounds__(NW * 64) void batch_kernel(const uint16_t *__restrict__ x, int64_t ldx,
+                                                       const int8_t *__restrict__ w, int64_t ldw,
+                                                       const float *__restrict__ scale,
+                                                       const void *__restrict__ bias, int bias_dt,
+                                                       uint16_t *__restrict__ y, int64_t ldy, int M, int N, int K,
+                                                       int kslice) {
+  using A = Act<DT>;
+  constexpr int KS = batch::KS;
+  // GU: N is the intermediate size I; tile t < RT holds gate rows, tile RT + t
+  // the matching up rows (weight rows N + n).
+  constexpr int NTW = GU ? 2 * RT : RT;  // 16-row weight tiles per wave
+  constexpr int WROWS = 16 * NTW;
+  constexpr int WL = WROWS / 8;  // 1 KB loads per stage (8 rows x 128 B each)
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * (16 * RT);
+  const int m0 = blockIdx.y * (16 * MT);
+
+  __shared__ __attribute__((aligned(16))) uint8_t tbuf[NW][WROWS * KS];
+
+  // Stage loads: load j covers wave rows 8j .. 8j+7; lane -> row 8j + lane/8,
+  // 16-byte chunk lane%8 of the row's 128-byte stage segment. Rows past N are
+  // clamped (loaded, never stored).
+  const int8_t *wsrc[WL];
+  uint32_t wdst[WL];
+#pragma unroll
+  for (int j = 0; j < WL; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    const int t = row >> 4;
+    int n = n0 + 16 * (t % RT) + (row & 15);
+    n = n < N ? n : N - 1;
+    if (t >= RT) n += N;
+    const int c = lane & 7;
+    wsrc[j] = w + (int64_t)n * ldw + 16 * c;
+    wdst[j] = (uint32_t)row * KS + (uint32_t)((c ^ ((row >> 1) & 7)) << 4);
+  }
+  // Activation fragment of lane (r, g): x[m0 + 16mt + r][k + 8g .. +7]; rows
+  // past M alias row 0 (their columns are never stored).
+  const uint16_t *xp[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = m0 + 16 * mt + r;
+    xp[mt] = x + (int64_t)(m < M ? m : 0) * ldx + 8 * g;
+  }
+  uint8_t *const slot = tbuf[wid];
+
+  const int kb = wid * kslice;
+  const int ke = min(K, kb + kslice);
+  const int nst = ke > kb ? (ke - kb) / KS : 0;
+
+  f32x4 acc[NTW][MT];
+#pragma unroll
+  for (int t = 0; t < NTW; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Ring of D stages in flight; stage st's weights and activation fragments
+  // sit in slot st % D (loaded D stages ahead).
+  uint4 wreg[D][WL];
+  uint4 xf[D][4][MT];
+#define RA_LOAD_STAGE(st_, SLOT_)                                                                   \
+  {                                                                                                 \
+    const int k_ = kb + KS * (st_);                                                                 \
+    const int slot_ = (SLOT_);                                                                      \
+    _Pragma("unroll") for (int j_ = 0; j_ < WL; ++j_) wreg[slot_][j_] =                             \
+        *reinterpret_cast<const uint4 *>(wsrc[j_] + k_);                                            \
+    _Pragma("unroll") for (int s_ = 0; s_ < 4; ++s_)                                                \
+        _Pragma("unroll") for (int mt_ = 0; mt_ < MT; ++mt_) xf[slot_][s_][mt_] =                   \
+            *reinterpret_cast<const uint4 *>(xp[mt_] + k_ + 32 * s_);                               \
+  }
+
+#pragma unroll
+  for (int p = 0; p < D; ++p)
+    if (p < nst) RA_LOAD_STAGE(p, p);
+
+  // Stage st_ in ring slot DP_ (= st_ % D; a literal after unrolling):
+  // transpose its weights through the wave's LDS slot (LDS executes a wave's
+  // accesses in order, so the reads see these writes and the next stage's
+  // writes cannot overtake the reads), multiply, then reload the slot with
+  // stage st_ + D.
+#define RA_BODY(st_, DP_)                                                                           \
+  {                                                                                                 \
+    _Pragma("unroll") for (int j = 0; j < WL; ++j)                                                  \
+        store16(slot + wdst[j], wreg[DP_][j]);                                                     \
+    _Pragma("unroll") for (int s = 0; s < 4; ++s) {                                                 \
+      _Pragma("unroll") for (int t = 0; t < NTW; ++t) {                                             \
+        const int row = 16 * t + r;                                                                 \
+        const int chunk = 2 * s + (g >> 1);                                                         \
+        const uint2 q = *reinterpret_cast<const uint2 *>(                                           \
+            slot + row * KS + ((chunk ^ ((row >> 1) & 7)) << 4) + 8 * (g & 1));                     \
+        const uint4 a = A::dq8(q.x, q.y);                                                           \
+        _Pragma("unroll") for (int mt = 0; mt < MT; ++mt) acc[t][mt] =                              \
+            A::mfma16(a, xf[DP_][s][mt], acc[t][mt]);                                               \
+      }                                                                                             \
+    }                                                                                               \
+    if ((st_) + D < nst) RA_LOAD_STAGE((st_) + D, DP_);                                             \
+  }
+
+  int st = 0;
+  for (; st + D <= nst; st += D) {
+#pragma unroll
+    for (int i = 0; i < D; ++i) RA_BODY(st + i, i);
+  }
+#pragma unroll
+  for (int i = 0; i < D; ++i)
+    if (st + i < nst) RA_BODY(st + i, i);
+#undef RA_BODY
+#undef RA_LOAD_STAGE
+
+  // Combine the NW split-K partial sums in a fixed order, then the epilogue.
+  // Output tile i = t*MT + mt (t < RT) is finished by wave i % NW.
+  constexpr int NACC = NTW * MT;
+  constexpr int NOUT = RT * MT;
+  __shared__ f32x4 red[NW > 1 ? NW : 1][NACC][64];
+  if (NW > 1) {
+#pragma unroll
+    for (int t = 0; t < NTW; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[wid][t * MT + mt][lane] = acc[t][mt];
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < NOUT; ++i) {
+    if (NW > 1 && (i % NW) != wid) continue;
+    const int t = i / MT, mt = i % MT;
+    f32x4 s = acc[t][mt];
+    f32x4 su = acc[GU ? RT + t : t][mt];
+    if (NW > 1) {
+      s = red[0][i][lane];
+      if (GU) su = red[0][(RT + t) * MT + mt][lane];
+#pragma unroll
+      for (int v = 1; v < NW; ++v) {
+        s += red[v][i][lane];
+        if (GU) su += red[v][(RT + t) * MT + mt][lane];
+      }
+    }
+    const int m = m0 + 16 * mt + r;
+    if (m >= M) continue;
+    uint16_t *yrow = y + (int64_t)m * ldy;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n0 + 16 * t + 4 * g + q;
+      if (n >= N) continue;
+      if (GU)
+        yrow[n] = swiglu_out<A>(s[q] * scale[n], su[q] * scale[N + n]);
+      else
+        yrow[n] = A::out(epilogue_value(s[q], scale, bias, bias_dt, n));
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Host side.
+// ----------------------------------------------------------------------------
+static bool batch_shape_ok(int x_dt, const void *x, int64_t ldx, const int8_t *w, int64_t ldw, int64_t M,
+                           int64_t N, int64_t K) {
+  if (x_dt != RA_F16 && x_dt != RA_BF16) return false;
+  if (M < 1 || M > batch::kMaxM || N > ((int64_t)1 << 30) || K > ((int64_t)1 << 30)) return false;
+  if (K < batch::KS || K % batch::KS != 0) return false;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w) & 15)) return false;
+  return (ldx % 8) == 0 && (ldw % 16) == 0;
+}
+
+bool batch_supported(const GemmArgs &a) { return batch_shape_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.M, a.N, a.K); }
+
+bool gateup_batch_supported(const GateUpArgs &a) {
+  return batch_shape_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.M, a.I, a.K);
+}
+
+template <int DT, int MT, int RT, int NW, bool GU>
+static void batch_go(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale, const void *bias,
+                     int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t s) {
+  constexpr int D = MT == 1 ? 4 : (MT == 2 ? 3 : 2);  // stages in flight (registers: D * (8 + 16 MT) per lane)
+  const int kslice = (int)(((K + NW - 1) / NW + batch::KS - 1) / batch::KS * batch::KS);
+  const dim3 grid((unsigned)((N + 16 * RT - 1) / (16 * RT)), (unsigned)((M + 16 * MT - 1) / (16 * MT)));
+  hipLaunchKernelGGL((batch_kernel<DT, MT, RT, NW, D, GU>), grid, dim3(NW * 64), 0, s,
+                     static_cast<const uint16_t *>(x), ldx, w, ldw, scale, bias, bias_dt, static_cast<uint16_t *>(y),
+                     ldy, (int)M, (int)N, (int)K, kslice);
+}
+
+// M tiles per workgroup: one 16-row activation tile up to M = 16, then the
+// whole batch in one workgroup (activations re-read once per weight tile).
+template <int DT, int RT, bool GU>
+static void batch_dispatch_rt(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
+                              const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                              hipStream_t s) {
+  if (M <= 16) batch_go<DT, 1, RT, 4, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  else if (M <= 32) batch_go<DT, 2, RT, 4, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  else batch_go<DT, 4, RT, 4, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+}
+
+static int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
+// Weight tiles per workgroup. Each workgroup streams its 16*RT rows (times 2
+// with the gate/up pair) and reads the whole activation block once, so the
+// cost per CU is the rows of its busiest share plus the activation bytes of
+// its workgroups (L2 hits, weighted 1/4 against HBM weight bytes):
+//   cost(RT) = max rows per CU + 1/4 * workgroups per CU * 2 * Mpad.
+// Measured on MI355X (K=4096 N=11008): M=16 15.0 us with RT=3 vs 18.5 with
+// RT=1; M=64 24.7 vs 52.6; (K=28672 N=8192 M=17) RT=2 56 us vs 66 with RT=3.
+static int batch_pick_rt(int64_t M, int64_t N, bool gu, int cus) {
+  const int64_t mpad = M <= 16 ? 16 : (M <= 32 ? 32 : 64);
+  int best = 1;
+  double best_c = 0;
+  for (int rt = 1; rt <= (gu ? 2 : 3); ++rt) {
+    if (gu && rt == 2 && mpad > 32) continue;  // register budget
+    const int64_t wgs = (N + 16 * rt - 1) / (16 * rt);
+    const int64_t per_cu = (wgs + cus - 1) / cus;
+    const double c = (double)(per_cu * 16 * rt * (gu ? 2 : 1)) + 0.25 * (double)(per_cu * 2 * mpad);
+    if (rt == 1 || c <= best_c) best = rt, best_c = c;
+  }
+  return best;
+}
+
+template <int DT, bool GU>
+static void batch_dispatch(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
+                           const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                           hipStream_t s) {
+  int rt = batch_pick_rt(M, N, GU, device_cus());
+#ifdef RA_TUNING
+  extern int g_batch_rt;
+  if (g_batch_rt > 0) rt = g_batch_rt;
+#endif
+  if constexpr (!GU) {
+    if (rt == 3) return batch_dispatch_rt<DT, 3, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  }
+  if (rt == 2 && !(GU && M > 32))
+    return batch_dispatch_rt<DT, 2, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  batch_dispatch_rt<DT, 1, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+}
+
+hipError_t batch_launch(const GemmArgs &a, hipStream_t s) {
+  if (a.x_dt == RA_F16)
+    batch_dispatch<RA_F16, false>(a.x, a.ldx, a.w, a.ldw, a.scale, a.bias, a.bias_dt, a.y, a.ldy, a.M, a.N, a.K, s);
+  else
+    batch_dispatch<RA_BF16, false>(a.x, a.ldx, a.w, a.ldw, a.scale, a.bias, a.bias_dt, a.y, a.ldy, a.M, a.N, a.K,
+                                   s);
+  return hipGetLastError();
+}
+
+hipError_t gateup_batch_launch(const GateUpArgs &a, hipStream_t s) {
+  if (a.x_dt == RA_F16)
+    batch_dispatch<RA_F16, true>(a.x, a.ldx, a.w, a.ldw, a.scale, nullptr, RA_F32, a.h, a.ldh, a.M, a.I, a.K, s);
+  else
+    batch_dispatch<RA_BF16, true>(a.x, a.ldx, a.w, a.ldw, a.scale, nullptr, RA_F32, a.h, a.ldh, a.M, a.I, a.K, s);
+  return hipGetLastError();
+}
+
+}  // namespace ra

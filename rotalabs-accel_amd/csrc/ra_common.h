@@ -2,12 +2,32 @@
 // int8 -> fp16/bf16 dequantisation, MFMA wrappers and dtype conversions.
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "rotaccel.h"
 
 namespace ra {
+
+// 16-byte store of a uint4 through a native vector type. (Assigning the HIP
+// uint4 struct through a cast pointer is lowered as a struct copy that keeps
+// the source array in scratch memory.)
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store16(void *p, const uint4 &v) {
+  *reinterpret_cast<u32x4_t *>(p) = u32x4_t{v.x, v.y, v.z, v.w};
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [LO, HI).
+template <int LO, int HI, typename F>
+__device__ __forceinline__ void static_for_int(F &&f) {
+  if constexpr (LO < HI) {
+    f(std::integral_constant<int, LO>{});
+    static_for_int<LO + 1, HI>(f);
+  }
+}
+
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));

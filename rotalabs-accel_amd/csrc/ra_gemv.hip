@@ -54,7 +54,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint16_t *__restrict__ 
   float *red = reinterpret_cast<float *>(slots + (size_t)nw * NLD * 1024);            // [nw][NT][M][16]
 
   const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n0 = blockIdx.x * 16 * RT;
   uint8_t *slot = slots + (size_t)wid * NLD * 1024;
 

@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t *__restri
   using A = Act<DT>;
   constexpr int NR = GU ? 2 * RW : RW;  // weight rows per wave: [r] gate/plain, [RW + r] up
   const int lane = threadIdx.x & 63;
-  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RW;
+  const int n0 = (blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * RW;
   if (n0 >= N) return;  // whole wave; no barriers in this kernel
   // Rows past N (last wave only) are clamped to N - 1: in bounds, never stored.
   const int8_t *wr[NR];
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(256) void gemv_rows_pipe_kernel(const uint16_t *__r
   using A = Act<DT>;
   constexpr int NT = GU ? 2 : 1;  // weight rows per output row: gate (and up)
   const int lane = threadIdx.x & 63;
-  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RP;
+  const int n0 = (blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * RP;
   if (n0 >= N) return;  // whole wave; no barriers in this kernel
   // Window c covers k = 1024c + 16*lane .. +15; lanes past K re-read the first
   // 16 elements of the row (offset 0 from the row start; K >= 16) and

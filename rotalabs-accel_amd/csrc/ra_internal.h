@@ -62,6 +62,13 @@ hipError_t gemv_rows_launch(const GemmArgs &a, hipStream_t s);
 bool gateup_gemv_rows_supported(const GateUpArgs &a);
 hipError_t gateup_gemv_rows_launch(const GateUpArgs &a, hipStream_t s);
 
+// Small-batch MFMA GEMM (M <= 64, K % 128 == 0): line-wide weight loads
+// transposed through LDS, split-K across the workgroup's waves.
+bool batch_supported(const GemmArgs &a);
+hipError_t batch_launch(const GemmArgs &a, hipStream_t s);
+bool gateup_batch_supported(const GateUpArgs &a);
+hipError_t gateup_batch_launch(const GateUpArgs &a, hipStream_t s);
+
 // Decode GEMV (M <= 4, x staged in LDS, one HBM round trip per wave).
 bool gemv_supported(const GemmArgs &a);
 hipError_t gemv_launch(const GemmArgs &a, hipStream_t s);

@@ -36,7 +36,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
   // tile RT + t hold matching gate / up rows.
   constexpr int NTW = GU ? 2 * RT : RT;
   const int lane = threadIdx.x & 63;
-  const int wid = threadIdx.x >> 6;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
   const int r = lane & 15;
   const int g = lane >> 4;
   const int n0 = blockIdx.x * (16 * RT);

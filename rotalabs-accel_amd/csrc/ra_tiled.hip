@@ -282,15 +282,6 @@ struct DmaTile {
   static_assert((S - 1) * COPIES <= 63, "vmcnt is a 6-bit counter");
 };
 
-// Compile-time loop: f(std::integral_constant<int, I>) for I in [LO, HI).
-template <int LO, int HI, typename F>
-__device__ __forceinline__ void static_for(F &&f) {
-  if constexpr (LO < HI) {
-    f(std::integral_constant<int, LO>{});
-    static_for<LO + 1, HI>(f);
-  }
-}
-
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -388,7 +379,7 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
   {                                                                                         \
     const int kofs_ = (kt_) * BK;                                                           \
     const uint32_t so_ = (uint32_t)(st_) * STAGE;                                           \
-    static_for<LO_, HI_>([&](auto ic_) {                                                    \
+    static_for_int<LO_, HI_>([&](auto ic_) {                                                    \
       constexpr int i = decltype(ic_)::value;                                               \
       constexpr bool isA = i < A_COPIES;                                                    \
       constexpr int li = isA ? i : i - A_COPIES;                                            \

@@ -25,7 +25,7 @@ ABI_VERSION = 1
 # enum ra_dtype
 F16, BF16, F32 = 0, 1, 2
 # enum ra_variant
-VARIANT_AUTO, VARIANT_SKINNY, VARIANT_TILED, VARIANT_GENERIC, VARIANT_GEMV, VARIANT_ROWS = 0, 1, 2, 3, 4, 5
+VARIANT_AUTO, VARIANT_SKINNY, VARIANT_TILED, VARIANT_GENERIC, VARIANT_GEMV, VARIANT_ROWS, VARIANT_BATCH = range(7)
 
 _DTYPE_CODE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
 

@@ -59,7 +59,7 @@ def test_argument_checks_without_device_work():
     assert lib.ra_w8a16_gemm_ex(p, 16, 0, p, 16, p, n, 0, p, 16, 1, 16, 16, 99, n) == 1
 
 
-@pytest.mark.parametrize("M,expect", [(1, 5), (2, 5), (3, 1), (4, 1), (5, 1), (16, 1), (64, 1), (65, 2), (2048, 2)])
+@pytest.mark.parametrize("M,expect", [(1, 5), (2, 5), (3, 6), (4, 6), (5, 6), (16, 6), (64, 6), (65, 2), (2048, 2)])
 def test_variant_selection(M, expect):
     assert _backend.load().ra_w8a16_gemm_select(M, 11008, 4096, 0) == expect
 
@@ -67,8 +67,8 @@ def test_variant_selection(M, expect):
 def test_variant_selection_fallbacks():
     lib = _backend.load()
     assert lib.ra_w8a16_gemm_select(1, 8192, 28672, 1) == 5  # row GEMV: any K
-    assert lib.ra_w8a16_gemm_select(3, 8192, 8192, 1) == 1   # M = 3..64: split-K MFMA (faster than the LDS GEMV)
-    assert lib.ra_w8a16_gemm_select(4, 8192, 28672, 1) == 1
+    assert lib.ra_w8a16_gemm_select(3, 8192, 8192, 1) == 6   # M = 3..64, K % 128 == 0: small-batch kernel
+    assert lib.ra_w8a16_gemm_select(4, 8192, 1040, 1) == 1   # K % 128 != 0: split-K MFMA kernel
     assert lib.ra_w8a16_gemm_select(1, 64, 50, 0) == 3     # K % 16 != 0 -> generic
     assert lib.ra_w8a16_gemm_select(1, 64, 64, 2) == 3     # fp32 activations -> generic
     assert lib.ra_w8a16_gemm_select(4, 64, 0, 0) == 3      # K == 0 -> generic (bias / zeros)
