@@ -18,6 +18,10 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void store16(void *p, const uint4 &v) {
   *reinterpret_cast<u32x4_t *>(p) = u32x4_t{v.x, v.y, v.z, v.w};
 }
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void store8(void *p, uint32_t lo, uint32_t hi) {
+  *reinterpret_cast<u32x2_t *>(p) = u32x2_t{lo, hi};
+}
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [LO, HI).
 template <int LO, int HI, typename F>

@@ -262,6 +262,24 @@ __device__ __forceinline__ void dma16(const void *g_minus_ofs, uint32_t m0_value
     asm volatile("global_load_lds_dwordx4 %0, off offset:%1" ::"v"(g_minus_ofs), "n"(OFS) : "memory");
 }
 
+// As dma16 with the uniform part of the global address in an SGPR pair and a
+// 32-bit per-lane byte offset, so a copy needs no per-lane address arithmetic.
+template <int OFS, bool NEW_M0>
+__device__ __forceinline__ void dma16s(const void *sbase, uint32_t voff, uint32_t m0_value) {
+  if (NEW_M0)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3" ::"s"(m0_value),
+                 "v"(voff), "s"(sbase), "n"(OFS)
+                 : "memory", "m0");
+  else
+    asm volatile("global_load_lds_dwordx4 %0, %1 offset:%2" ::"v"(voff), "s"(sbase), "n"(OFS) : "memory");
+}
+
+// Largest byte offset the 32-bit per-lane copy offsets may reach (the copy
+// bases are moved down by DMA_BIAS so that offsets minus the instruction
+// offset stay non-negative).
+constexpr int DMA_BIAS = 3072;
+constexpr uint64_t DMA_SPAN = (uint64_t)0xFFFFFFFFu - 2 * DMA_BIAS;
+
 // Tile geometry of the direct-to-LDS kernel: 4 waves in a 2 x 2 grid, each
 // owning BMB x BNB blocks of 32 x 32 outputs (one v_mfma_f32_32x32x16 per
 // block and 16-deep K sub-step). Bigger per-wave tiles need fewer LDS bytes
@@ -337,18 +355,20 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
   // ---- copy sources: A copy i covers tile rows 8*ai .. +7 (ai = A_COPIES*wid
   // + i), lane -> row 8*ai + lane/8, LDS chunk lane%8 <- global chunk
   // (lane%8) ^ ((row>>1)&7). Rows past M are clamped (loaded, never stored).
-  const uint16_t *a_src[A_COPIES];
+  // Per-lane byte offsets from the copy bases xb / wb (moved down by
+  // DMA_BIAS; the host keeps every offset below 2^32).
+  uint32_t a_voff[A_COPIES];
 #pragma unroll
   for (int i = 0; i < A_COPIES; ++i) {
     const int row = 8 * (A_COPIES * wid + i) + (lane >> 3);
     const int c = (lane & 7) ^ ((row >> 1) & 7);
     int gr = m0 + row;
     gr = gr < M ? gr : M - 1;
-    a_src[i] = x + (int64_t)gr * ldx + c * 8 - (i % 4) * 512;  // - instruction offset (bytes / 2)
+    a_voff[i] = (uint32_t)(((int64_t)gr * ldx + c * 8) * 2) + (uint32_t)(DMA_BIAS - (i % 4) * 1024);
   }
   // B copy i covers tile rows 16*bi .. +15 (bi = B_COPIES*wid + i), lane ->
   // row 16*bi + lane/4, LDS chunk lane%4 <- global chunk (lane%4)^((row>>2)&3).
-  const int8_t *b_src[B_COPIES];
+  uint32_t b_voff[B_COPIES];
 #pragma unroll
   for (int i = 0; i < B_COPIES; ++i) {
     const int row = 16 * (B_COPIES * wid + i) + (lane >> 2);
@@ -363,8 +383,10 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
       wr = n0 + row;
       wr = wr < N ? wr : N - 1;
     }
-    b_src[i] = w + (int64_t)wr * ldw + c * 16 - (i % 4) * 1024;  // - instruction offset
+    b_voff[i] = (uint32_t)((int64_t)wr * ldw + c * 16) + (uint32_t)(DMA_BIAS - (i % 4) * 1024);
   }
+  const char *const xb = reinterpret_cast<const char *>(x) - DMA_BIAS;
+  const char *const wb = reinterpret_cast<const char *>(w) - DMA_BIAS;
   const uint32_t lds0 = lds_offset(lds);
   const uint32_t a_dst = lds0 + (uint32_t)(A_COPIES * wid) * 1024;
   const uint32_t b_dst = lds0 + A_BYTES + (uint32_t)(B_COPIES * wid) * 1024;
@@ -372,12 +394,13 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
 // Copies [LO_, HI_) of K tile kt_ into stage st_ (copies 0..A_COPIES-1 are
 // the A copies, the rest the B copies).
 // A copy's local index li (within A or B) selects M0 group li/4 and
-// instruction offset (li%4)*1024; the copy sources are stored pre-adjusted by
-// -(li%4)*1024 bytes. M0 is written at the first copy of a part and of each
-// group.
+// instruction offset (li%4)*1024; the per-lane offsets are stored
+// pre-adjusted by -(li%4)*1024 bytes. M0 is written at the first copy of a
+// part and of each group. The K tile's byte offset goes into the SGPR base.
 #define RA_ISSUE_PART(kt_, st_, LO_, HI_)                                                   \
   {                                                                                         \
-    const int kofs_ = (kt_) * BK;                                                           \
+    const char *sa_ = xb + (int64_t)(kt_) * (2 * BK);                                       \
+    const char *sb_ = wb + (int64_t)(kt_) * BK;                                             \
     const uint32_t so_ = (uint32_t)(st_) * STAGE;                                           \
     static_for_int<LO_, HI_>([&](auto ic_) {                                                    \
       constexpr int i = decltype(ic_)::value;                                               \
@@ -386,9 +409,9 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
       constexpr bool fresh = i == (LO_) || i == A_COPIES || li % 4 == 0;                    \
       const uint32_t m0v = (isA ? a_dst : b_dst) + so_ + (uint32_t)(li / 4) * 4096;         \
       if constexpr (isA)                                                                    \
-        dma16<(li % 4) * 1024, fresh>(a_src[li] + kofs_, m0v);                              \
+        dma16s<(li % 4) * 1024, fresh>(sa_, a_voff[li], m0v);                              \
       else                                                                                  \
-        dma16<(li % 4) * 1024, fresh>(b_src[li] + kofs_, m0v);                              \
+        dma16s<(li % 4) * 1024, fresh>(sb_, b_voff[li], m0v);                              \
     });                                                                                     \
   }
 #define RA_ISSUE(kt_, st_) RA_ISSUE_PART(kt_, st_, 0, COPIES)
@@ -414,15 +437,18 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
   const int b_sw = (l32 >> 2) & 3;
 
   // Software pipeline at sub-step granularity (4 sub-steps of 16 k per K
-  // tile), with the order pinned by scheduling barriers so that LDS latency
-  // and dequantisation hide under the MFMAs:
-  //   sub-step ss: [LDS reads for ss+1] | [MFMAs of ss, interleaved 1:1 with
-  //   the dequantisation of ss+1's B fragments]
+  // tile), with the order pinned by scheduling groups so that LDS latency and
+  // dequantisation hide under the MFMAs. Sub-step ss issues its copies, then
+  // its 16-ish MFMAs with the LDS reads for ss+1 slotted one after each of
+  // the first MFMAs (a burst of reads stalls the wave behind the LDS queue)
+  // and three dequantisation VALU instructions after each MFMA.
   // A fragments ping-pong in fa[2]; the raw 16-byte B fragments of sub-step
   // pair p sit in fbr[p] (pair 1 is read during sub-step 0, pair 0 of the
   // next tile during sub-step 3); dequantised B ping-pongs in bq[2]. The tile
-  // boundary (wait for the next tile's copies, barrier, next copy, first
-  // reads of the next tile) opens sub-step 3.
+  // boundary (wait for the next tile's copies, barrier, first reads of the
+  // next tile) opens sub-step 3. Stage indices are compile-time constants in
+  // the steady state, so every LDS address is a base register plus an
+  // immediate offset.
   uint4 fa[2][BMB], fbr[2][BNB], bq[2][BNB];
 #define RA_READ_A(st_, ss_, FA)                                                                     \
   {                                                                                                 \
@@ -442,62 +468,62 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
 #define RA_MMA(FA, BQ)                                                                              \
   _Pragma("unroll") for (int bi = 0; bi < BMB; ++bi)                                                \
       _Pragma("unroll") for (int bj = 0; bj < BNB; ++bj) acc[bi][bj] = Ac::mfma32(FA[bi], BQ[bj], acc[bi][bj]);
-// Interleave the BMB*BNB MFMAs with the dequantisation VALU work.
-#define RA_INTERLEAVE()                                                                             \
-  _Pragma("unroll") for (int i_ = 0; i_ < BMB * BNB; ++i_) {                                        \
+// The BMB*BNB MFMAs of a sub-step: one LDS read after each of the first NR_,
+// three VALU instructions after each.
+#define RA_INTERLEAVE(NR_)                                                                          \
+  static_for_int<0, BMB * BNB>([&](auto ic_) {                                                      \
+    constexpr int i_ = decltype(ic_)::value;                                                        \
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                              \
+    if constexpr (i_ < (NR_)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                    \
     __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);                                              \
-  }                                                                                                 \
-  __builtin_amdgcn_sched_barrier(0);
-// Sub-step 3: the dequantisation needs B fragments read at the start of the
-// sub-step, so the first half of the MFMAs runs before it.
-#define RA_INTERLEAVE_LATE()                                                                        \
-  __builtin_amdgcn_sched_group_barrier(0x008, (BMB * BNB) / 2, 0);                                  \
-  _Pragma("unroll") for (int i_ = 0; i_ < BMB * BNB - (BMB * BNB) / 2; ++i_) {                      \
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                              \
-    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);                                              \
-  }                                                                                                 \
+  });                                                                                               \
   __builtin_amdgcn_sched_barrier(0);
 // Sub-steps 0..2 of the tile in stage st_; with ISSUE_, the copies of tile
 // ikt_ into stage ist_ are issued in three parts.
 #define RA_SUBSTEPS_012(st_, ISSUE_, ikt_, ist_)                                                    \
-  RA_READ_A(st_, 1, fa[1]);                                                                         \
-  RA_READ_B(st_, 1, fbr[1]);                                                                        \
   if (ISSUE_) RA_ISSUE_PART(ikt_, ist_, 0, P1);                                                     \
   __builtin_amdgcn_sched_barrier(0);                                                                \
+  RA_READ_A(st_, 1, fa[1]);                                                                         \
+  RA_READ_B(st_, 1, fbr[1]);                                                                        \
   RA_MMA(fa[0], bq[0]);                                                                             \
   RA_DEQ(1, fbr[0], bq[1]);                                                                         \
-  RA_INTERLEAVE();                                                                                  \
-  RA_READ_A(st_, 2, fa[0]);                                                                         \
+  RA_INTERLEAVE(BMB + BNB);                                                                         \
   if (ISSUE_) RA_ISSUE_PART(ikt_, ist_, P1, P2);                                                    \
   __builtin_amdgcn_sched_barrier(0);                                                                \
+  RA_READ_A(st_, 2, fa[0]);                                                                         \
   RA_MMA(fa[1], bq[1]);                                                                             \
   RA_DEQ(0, fbr[1], bq[0]);                                                                         \
-  RA_INTERLEAVE();                                                                                  \
-  RA_READ_A(st_, 3, fa[1]);                                                                         \
+  RA_INTERLEAVE(BMB);                                                                               \
   if (ISSUE_) RA_ISSUE_PART(ikt_, ist_, P2, COPIES);                                                \
   __builtin_amdgcn_sched_barrier(0);                                                                \
+  RA_READ_A(st_, 3, fa[1]);                                                                         \
   RA_MMA(fa[0], bq[0]);                                                                             \
   RA_DEQ(1, fbr[1], bq[1]);                                                                         \
-  RA_INTERLEAVE();
+  RA_INTERLEAVE(BMB);
 // Tile boundary + sub-step 3: this tile's LDS reads are complete; wait until
 // only the copies of tiles younger than kt_+1 are in flight, then the barrier
 // makes tile kt_+1 visible and frees stage st_ (for tile kt_+S, copied during
-// the next tile); then the first reads of tile kt_+1 and the last MFMAs of
-// tile kt_, with the dequantisation of tile kt_+1's first B fragments.
+// the next tile); then the last MFMAs of tile kt_ with the first reads of
+// tile kt_+1 (B first: the dequantisation of its first B fragments, after
+// half the MFMAs, needs them).
 #define RA_BOUNDARY_SUBSTEP3(kt_, st_, YOUNGER_)                                                    \
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                                \
   wait_tiles<COPIES>(YOUNGER_);                                                                     \
   asm volatile("s_barrier" ::: "memory");                                                           \
   {                                                                                                 \
     const int sn_ = ((kt_) + 1) % S;                                                                \
-    RA_READ_A(sn_, 0, fa[0]);                                                                       \
     RA_READ_B(sn_, 0, fbr[0]);                                                                      \
+    RA_READ_A(sn_, 0, fa[0]);                                                                       \
   }                                                                                                 \
-  __builtin_amdgcn_sched_barrier(0);                                                                \
   RA_MMA(fa[1], bq[1]);                                                                             \
   RA_DEQ(0, fbr[0], bq[0]);                                                                         \
-  RA_INTERLEAVE_LATE();
+  static_for_int<0, BMB * BNB>([&](auto ic_) {                                                      \
+    constexpr int i_ = decltype(ic_)::value;                                                        \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                              \
+    if constexpr (i_ < BMB + BNB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                \
+    if constexpr (i_ >= (BMB * BNB) / 2) __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);         \
+  });                                                                                               \
+  __builtin_amdgcn_sched_barrier(0);
 
   const int KT = K / BK;
 #pragma unroll
@@ -515,11 +541,25 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
     RA_BOUNDARY_SUBSTEP3(0, 0, min(KT - 2, S - 2));
     // Steady state: tile kt copies tile kt+S-1 into the stage freed at the
     // last boundary; at its own boundary S-2 younger tiles are in flight.
-    for (kt = 1; kt <= KT - S; ++kt) {
-      const int st = kt % S;
-      RA_SUBSTEPS_012(st, true, kt + S - 1, (kt - 1) % S);
-      RA_BOUNDARY_SUBSTEP3(kt, st, S - 2);
+    // Unrolled by S (stage kt % S known at compile time).
+    auto steady = [&](auto stc, int ktv) __attribute__((always_inline)) {
+      constexpr int st = decltype(stc)::value;
+      RA_SUBSTEPS_012(st, true, ktv + S - 1, (st + S - 1) % S);
+      RA_BOUNDARY_SUBSTEP3(ktv, st, S - 2);
+    };
+    for (kt = 1; kt + S <= KT - S + 1; kt += S) {
+      static_for_int<0, S>([&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        steady(std::integral_constant<int, (1 + j) % S>{}, kt + j);
+      });
     }
+    static_for_int<0, S - 1>([&](auto jc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value;
+      if (kt <= KT - S) {
+        steady(std::integral_constant<int, (1 + j) % S>{}, kt);
+        ++kt;
+      }
+    });
     // Drain: every copy is issued.
     for (; kt < KT - 1; ++kt) {
       const int st = kt % S;
@@ -536,7 +576,6 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
   }
 #undef RA_BOUNDARY_SUBSTEP3
 #undef RA_SUBSTEPS_012
-#undef RA_INTERLEAVE_LATE
 #undef RA_INTERLEAVE
 #undef RA_DEQ
 #undef RA_MMA
@@ -625,17 +664,39 @@ bool tiled_supported(const GemmArgs &a) {
   return tiled_shape_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.ldy, a.M, a.N, a.K);
 }
 
+// The copies address x and w through 32-bit per-lane byte offsets: a launch
+// covers at most DMA_SPAN bytes of each. Larger operands are split into row
+// chunks of x (and, without the gate/up pairing, of w), one launch each.
+static bool dma_span_ok(bool gu, int64_t ldx, int64_t ldw, int64_t N, int64_t K, int bm) {
+  if ((uint64_t)((bm - 1) * ldx + K) * 2 > DMA_SPAN) return false;  // one row tile of x
+  const int64_t wrows = gu ? 2 * N : 256;                            // gate/up: both halves in one launch
+  return (uint64_t)((wrows - 1) * ldw + K) <= DMA_SPAN;
+}
+
 template <int DT, bool GU, int BMB, int BNB>
 static void launch_dma(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
                        const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                        hipStream_t s) {
   using G = DmaTile<BMB, BNB>;
   constexpr int OUTN = GU ? G::BN / 2 : G::BN;
-  const int tiles_m = (int)((M + G::BM - 1) / G::BM);
-  const int tiles_n = (int)((N + OUTN - 1) / OUTN);
-  hipLaunchKernelGGL((tiled_dma_kernel<DT, GU, BMB, BNB>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s,
-                     static_cast<const uint16_t *>(x), ldx, w, ldw, scale, bias, bias_dt,
-                     static_cast<uint16_t *>(y), ldy, (int)M, (int)N, (int)K, tiles_m, tiles_n);
+  // Rows of x (multiple of BM) and rows of w (multiple of OUTN) per launch.
+  const int64_t mc = std::max<int64_t>(G::BM, ((int64_t)((DMA_SPAN / 2 - K) / ldx) + 1) / G::BM * G::BM);
+  const int64_t nc = GU ? N : std::max<int64_t>(OUTN, ((int64_t)((DMA_SPAN - K) / ldw) + 1) / OUTN * OUTN);
+  const size_t bias_sz = bias_dt == RA_F32 ? 4 : 2;
+  for (int64_t ms = 0; ms < M; ms += mc) {
+    for (int64_t ns = 0; ns < N; ns += nc) {
+      const int64_t Mi = std::min(mc, M - ms), Ni = std::min(nc, N - ns);
+      const uint16_t *xi = static_cast<const uint16_t *>(x) + ms * ldx;
+      uint16_t *yi = static_cast<uint16_t *>(y) + ms * ldy + ns;
+      const float *si = scale + ns;
+      const void *bi = bias ? static_cast<const void *>(static_cast<const char *>(bias) + ns * bias_sz) : nullptr;
+      const int tiles_m = (int)((Mi + G::BM - 1) / G::BM);
+      const int tiles_n = (int)((Ni + OUTN - 1) / OUTN);
+      hipLaunchKernelGGL((tiled_dma_kernel<DT, GU, BMB, BNB>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s,
+                         xi, ldx, w + ns * ldw, ldw, si, bi, bias_dt, yi, ldy, (int)Mi, (int)Ni, (int)K, tiles_m,
+                         tiles_n);
+    }
+  }
 }
 
 // Direct-to-LDS tile shapes, (BMB, BNB) = per-wave 32x32 blocks, and a
@@ -699,9 +760,10 @@ static hipError_t launch(const void *x, int64_t ldx, int x_dt, const int8_t *w, 
 #ifdef RA_TUNING
   extern int g_tiled_mode;  // 0 auto, 1 register-staged kernel, 2 direct-to-LDS auto, 3.. forced shapes
   forced = g_tiled_mode;
-  const bool use_dma = g_tiled_mode >= 2 || (g_tiled_mode == 0 && K % tiled::BK == 0);
+  const bool use_dma = (g_tiled_mode >= 2 || (g_tiled_mode == 0 && K % tiled::BK == 0)) &&
+                       dma_span_ok(GU, ldx, ldw, N, K, 256);
 #else
-  const bool use_dma = K % tiled::BK == 0;
+  const bool use_dma = K % tiled::BK == 0 && dma_span_ok(GU, ldx, ldw, N, K, 256);
 #endif
   if (use_dma) {
     if (x_dt == RA_F16)
