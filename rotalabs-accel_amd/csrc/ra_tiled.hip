@@ -274,11 +274,12 @@ __device__ __forceinline__ void dma16s(const void *sbase, uint32_t voff, uint32_
     asm volatile("global_load_lds_dwordx4 %0, %1 offset:%2" ::"v"(voff), "s"(sbase), "n"(OFS) : "memory");
 }
 
-// Largest byte offset the 32-bit per-lane copy offsets may reach (the copy
+// Largest byte offset the 32-bit per-lane copy offsets may reach. The copy
 // bases are moved down by DMA_BIAS so that offsets minus the instruction
-// offset stay non-negative).
+// offset stay non-negative, and offsets stay below 2^31 so that they mean
+// the same whether the address unit reads them as signed or unsigned.
 constexpr int DMA_BIAS = 3072;
-constexpr uint64_t DMA_SPAN = (uint64_t)0xFFFFFFFFu - 2 * DMA_BIAS;
+constexpr uint64_t DMA_SPAN = (uint64_t)0x7FFFFFFF - 2 * DMA_BIAS;
 
 // Tile geometry of the direct-to-LDS kernel: 4 waves in a 2 x 2 grid, each
 // owning BMB x BNB blocks of 32 x 32 outputs (one v_mfma_f32_32x32x16 per
@@ -664,7 +665,7 @@ bool tiled_supported(const GemmArgs &a) {
   return tiled_shape_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.ldy, a.M, a.N, a.K);
 }
 
-// The copies address x and w through 32-bit per-lane byte offsets: a launch
+// The copies address x and w through 31-bit per-lane byte offsets: a launch
 // covers at most DMA_SPAN bytes of each. Larger operands are split into row
 // chunks of x (and, without the gate/up pairing, of w), one launch each.
 static bool dma_span_ok(bool gu, int64_t ldx, int64_t ldw, int64_t N, int64_t K, int bm) {

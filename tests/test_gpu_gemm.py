@@ -236,6 +236,46 @@ def test_strided_and_misaligned_inputs(gpu):
     _oracle_check(y4, c2.x, c2.q, c2.s)
 
 
+def _strided_on(gpu, t, ld):
+    """A (rows, cols) view of t on the GPU with row stride ld elements."""
+    rows, cols = t.shape
+    store = torch.empty((rows - 1) * ld + cols, dtype=t.dtype, device=gpu)
+    v = store.as_strided((rows, cols), (ld, 1))
+    v.copy_(t.to(gpu))
+    return v
+
+
+def test_operands_spanning_more_than_2gib(gpu):
+    """Activations and weights whose rows span more than 2^31 bytes: the
+    prefill kernel addresses its copies through 31-bit offsets, so such
+    operands are split into row chunks, one launch each (x: 512 + 88 rows,
+    W: 256 + 256 + 88 rows)."""
+    M, K, N = 600, 256, 600
+    c = gemm_case(M, K, N, seed=11)
+    x = _strided_on(gpu, c.x, (1 << 21) + 64)     # 4 MiB per activation row, ~2.5 GB
+    w = _strided_on(gpu, c.q, (1 << 23) + 16)     # 8 MiB per weight row, ~5 GB
+    y = _run(x, w, c.s.to(gpu)).cpu()
+    del x, w
+    torch.cuda.empty_cache()
+    _oracle_check(y, c.x, c.q, c.s)
+
+
+def test_gateup_weights_spanning_more_than_2gib(gpu):
+    """A gate/up weight pair spanning more than 2^31 bytes runs the
+    register-staged kernel (64-bit addresses) and matches the unfused path."""
+    M, K, inter = 300, 256, 300
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(M, K, generator=g).half()
+    q, s = ra.quantize_weight_per_channel(torch.randn(2 * inter, K, generator=g) * 0.02)
+    w = _strided_on(gpu, q, (1 << 22) + 16)       # 4 MiB per weight row, ~2.5 GB
+    h = ra.int8_gateup_swiglu(x.to(gpu), w, s.to(gpu)).cpu()
+    del w
+    torch.cuda.empty_cache()
+    gu = ra.int8_gemm(x.to(gpu), q.to(gpu), s.to(gpu))
+    h2 = ra.swiglu_fused(gu[:, :inter].contiguous(), gu[:, inter:].contiguous()).cpu()
+    torch.testing.assert_close(h.float(), h2.float(), rtol=1e-2, atol=1e-2)
+
+
 def test_batched_leading_dims_and_modules(gpu):
     g = torch.Generator().manual_seed(4)
     lin = torch.nn.Linear(256, 320, bias=True)
