@@ -281,14 +281,17 @@ __device__ __forceinline__ void dma16s(const void *sbase, uint32_t voff, uint32_
 constexpr int DMA_BIAS = 3072;
 constexpr uint64_t DMA_SPAN = (uint64_t)0x7FFFFFFF - 2 * DMA_BIAS;
 
-// Tile geometry of the direct-to-LDS kernel: 4 waves in a 2 x 2 grid, each
-// owning BMB x BNB blocks of 32 x 32 outputs (one v_mfma_f32_32x32x16 per
+// Tile geometry of the direct-to-LDS kernel: 4 waves in a WR x (4/WR) grid,
+// each owning BMB x BNB blocks of 32 x 32 outputs (one v_mfma_f32_32x32x16 per
 // block and 16-deep K sub-step). Bigger per-wave tiles need fewer LDS bytes
-// per MFMA: (4,2) reads 0.625 KB per MFMA, (3,4) 0.417, (4,4) 0.375.
-template <int BMB, int BNB>
+// per MFMA: (4,2) reads 0.625 KB per MFMA, (3,4) 0.417, (4,4) 0.375. With one
+// wave row (WR = 1) every weight column is dequantised by one wave instead
+// of two, for 50 % more activation reads: 256x256 as (8,2) in 1 x 4 measured
+// 1-2 % faster than (4,4) in 2 x 2.
+template <int BMB, int BNB, int WR>
 struct DmaTile {
   static constexpr int WM = 32 * BMB, WN = 32 * BNB;  // per-wave sub-tile
-  static constexpr int BM = 2 * WM, BN = 2 * WN, BK = 64;
+  static constexpr int BM = WR * WM, BN = (4 / WR) * WN, BK = 64;
   static constexpr int A_BYTES = BM * BK * 2;  // fp16/bf16 rows of 128 B
   static constexpr int B_BYTES = BN * BK;      // int8 rows of 64 B
   static constexpr int STAGE = A_BYTES + B_BYTES;
@@ -316,14 +319,14 @@ __device__ __forceinline__ void wait_tiles(int younger) {
   else wait_vmcnt<0>();
 }
 
-template <int DT, bool GU, int BMB, int BNB>
+template <int DT, bool GU, int BMB, int BNB, int WR>
 __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__restrict__ x, int64_t ldx,
                                                            const int8_t *__restrict__ w, int64_t ldw,
                                                            const float *__restrict__ scale,
                                                            const void *__restrict__ bias, int bias_dt,
                                                            uint16_t *__restrict__ y, int64_t ldy, int M, int N,
                                                            int K, int tiles_m, int tiles_n) {
-  using G = DmaTile<BMB, BNB>;
+  using G = DmaTile<BMB, BNB, WR>;
   using Ac = Act<DT>;
   constexpr int BM = G::BM, BN = G::BN, BK = G::BK, WM = G::WM, WN = G::WN, S = G::S;
   constexpr int A_COPIES = G::A_COPIES, B_COPIES = G::B_COPIES, COPIES = G::COPIES;
@@ -350,7 +353,7 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wid >> 1, wn = wid & 1;
+  const int wm = wid / (4 / WR), wn = wid % (4 / WR);
   const int l32 = lane & 31, g = lane >> 5;
 
   // ---- copy sources: A copy i covers tile rows 8*ai .. +7 (ai = A_COPIES*wid
@@ -674,11 +677,11 @@ static bool dma_span_ok(bool gu, int64_t ldx, int64_t ldw, int64_t N, int64_t K,
   return (uint64_t)((wrows - 1) * ldw + K) <= DMA_SPAN;
 }
 
-template <int DT, bool GU, int BMB, int BNB>
+template <int DT, bool GU, int BMB, int BNB, int WR>
 static void launch_dma(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
                        const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                        hipStream_t s) {
-  using G = DmaTile<BMB, BNB>;
+  using G = DmaTile<BMB, BNB, WR>;
   constexpr int OUTN = GU ? G::BN / 2 : G::BN;
   // Rows of x (multiple of BM) and rows of w (multiple of OUTN) per launch.
   const int64_t mc = std::max<int64_t>(G::BM, ((int64_t)((DMA_SPAN / 2 - K) / ldx) + 1) / G::BM * G::BM);
@@ -693,22 +696,25 @@ static void launch_dma(const void *x, int64_t ldx, const int8_t *w, int64_t ldw,
       const void *bi = bias ? static_cast<const void *>(static_cast<const char *>(bias) + ns * bias_sz) : nullptr;
       const int tiles_m = (int)((Mi + G::BM - 1) / G::BM);
       const int tiles_n = (int)((Ni + OUTN - 1) / OUTN);
-      hipLaunchKernelGGL((tiled_dma_kernel<DT, GU, BMB, BNB>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s,
+      hipLaunchKernelGGL((tiled_dma_kernel<DT, GU, BMB, BNB, WR>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s,
                          xi, ldx, w + ns * ldw, ldw, si, bi, bias_dt, yi, ldy, (int)Mi, (int)Ni, (int)K, tiles_m,
                          tiles_n);
     }
   }
 }
 
-// Direct-to-LDS tile shapes, (BMB, BNB) = per-wave 32x32 blocks, and a
-// relative cost per output element of a full tile, measured on MI355X with
-// whole rounds of tiles (M=8192 K=4096 N=4096 and the 70B MLP shapes): (4,4)
-// reaches ~1130 TFLOP/s, (4,3) ~1025, (3,4) ~995, (4,2) ~885.
+// Direct-to-LDS tile shapes, (BMB, BNB, WR) = per-wave 32x32 blocks and wave
+// rows, and a relative cost per output element of a full tile, measured on
+// MI355X with whole rounds of tiles (M=8192 K=4096 N=4096 and the 70B MLP
+// shapes): 256x256 reaches ~1330 TFLOP/s, 256x192 ~1240, 192x256 ~1180,
+// 256x128 ~1040.
 struct DmaShape {
-  int bmb, bnb;
+  int bmb, bnb, wr;
   double cost;
+  int64_t bm() const { return 32 * bmb * wr; }
+  int64_t bn() const { return 32 * bnb * (4 / wr); }
 };
-constexpr DmaShape kDmaShapes[] = {{4, 4, 1.00}, {4, 3, 1.10}, {3, 4, 1.13}, {4, 2, 1.28}};
+constexpr DmaShape kDmaShapes[] = {{8, 2, 1, 1.00}, {4, 3, 2, 1.10}, {3, 4, 2, 1.13}, {4, 2, 2, 1.28}};
 
 // One workgroup per CU (160 KB LDS), so tiles run in rounds of `cus`; pick
 // the shape with the least (rounds x tile area x cost).
@@ -718,7 +724,7 @@ static DmaShape pick_dma_shape(int64_t M, int64_t N, bool gu, int cus) {
   bool first = true;
   for (const DmaShape &c : kDmaShapes) {
     if (gu && c.bnb % 2) continue;
-    const int64_t bm = 64 * c.bmb, bn = 64 * c.bnb, outn = gu ? bn / 2 : bn;
+    const int64_t bm = c.bm(), bn = c.bn(), outn = gu ? bn / 2 : bn;
     const int64_t tiles = ((M + bm - 1) / bm) * ((N + outn - 1) / outn);
     const int64_t rounds = (tiles + cus - 1) / cus;
     const double t = (double)rounds * (double)(bm * bn) * c.cost;
@@ -740,17 +746,21 @@ static void launch_dma_auto(const void *x, int64_t ldx, const int8_t *w, int64_t
                             const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                             hipStream_t s, int forced) {
   DmaShape c = pick_dma_shape(M, N, GU, device_cus());
-  if (forced == 3) c = {4, 2, 0};
-  if (forced == 4) c = {3, 4, 0};
-  if (forced == 5) c = {4, 4, 0};
-  if (forced == 6 && !GU) c = {4, 3, 0};
-  if (c.bmb == 4 && c.bnb == 4) return launch_dma<DT, GU, 4, 4>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
-  if (c.bmb == 3 && c.bnb == 4) return launch_dma<DT, GU, 3, 4>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  if (forced == 3) c = {4, 2, 2, 0};
+  if (forced == 4) c = {3, 4, 2, 0};
+  if (forced == 5) c = {8, 2, 1, 0};
+  if (forced == 6 && !GU) c = {4, 3, 2, 0};
+#ifdef RA_TUNING
+  if (forced == 7) return launch_dma<DT, GU, 4, 4, 2>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+#endif
+  if (c.wr == 1) return launch_dma<DT, GU, 8, 2, 1>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  if (c.bmb == 3 && c.bnb == 4)
+    return launch_dma<DT, GU, 3, 4, 2>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
   if constexpr (!GU) {
     if (c.bmb == 4 && c.bnb == 3)
-      return launch_dma<DT, GU, 4, 3>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+      return launch_dma<DT, GU, 4, 3, 2>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
   }
-  launch_dma<DT, GU, 4, 2>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  launch_dma<DT, GU, 4, 2, 2>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
 }
 
 template <bool GU>
@@ -759,7 +769,7 @@ static hipError_t launch(const void *x, int64_t ldx, int x_dt, const int8_t *w, 
                          int64_t M, int64_t N, int64_t K, hipStream_t s) {
   int forced = 0;
 #ifdef RA_TUNING
-  extern int g_tiled_mode;  // 0 auto, 1 register-staged kernel, 2 direct-to-LDS auto, 3.. forced shapes
+  extern int g_tiled_mode;  // 0 auto, 1 register-staged kernel, 2 direct-to-LDS auto, 3.. forced shapes (5 = 256x256 1x4, 7 = 256x256 2x2)
   forced = g_tiled_mode;
   const bool use_dma = (g_tiled_mode >= 2 || (g_tiled_mode == 0 && K % tiled::BK == 0)) &&
                        dma_span_ok(GU, ldx, ldw, N, K, 256);
