@@ -286,6 +286,22 @@ def run_mlp(args, dev):
         out[f"M={M}"] = rec
         log(f"mlp M={M} H={H} I={I} bf16: {rec}")
         del x
+    # RMSNorm of x + residual (the block's prologue in a decoder layer), HBM-bound:
+    # reads x, residual, weight, writes y; 3 input sets (384 MiB) cycled so the
+    # reads come from HBM, not the 256 MB Infinity Cache.
+    M = 4096
+    xs = [torch.randn(M, H, device=dev, generator=g).to(torch.bfloat16) for _ in range(3)]
+    rs = [torch.randn(M, H, device=dev, generator=g).to(torch.bfloat16) for _ in range(3)]
+
+    class _Norm:
+        def run(self, n):
+            for i in range(n):
+                ra.rmsnorm_residual_fused(xs[i % 3], rs[i % 3], norm_w)
+    ms, _ = time_graph(_Norm(), 30, 9, per_graph=9)
+    gbs = (6 * M * H + 2 * H) / (ms * 1e-3) / 1e9
+    rec = {"us_per_call": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+    out[f"rmsnorm_residual M={M}"] = rec
+    log(f"rmsnorm_residual M={M} H={H} bf16: {rec}")
     return out
 
 

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define RA_ABI_VERSION 1
+#define RA_ABI_VERSION 2
 
 enum ra_dtype { RA_F16 = 0, RA_BF16 = 1, RA_F32 = 2 };
 
@@ -120,6 +120,22 @@ int ra_rmsnorm(const void *x, int64_t ldx, int x_dtype,
                const void *weight, int w_dtype,
                void *y, int64_t ldy, int y_dtype,
                int64_t rows, int64_t hidden, float eps, void *stream);
+
+/*
+ * ra_rmsnorm of v = x + residual, the sum rounded to the promotion of x_dtype
+ * and r_dtype (as rmsnorm_residual_torch computes (x + residual).float(),
+ * src/rotalabs_accel/kernels/normalization.py:48-64); the normalised value
+ * is rounded to x_dtype, then multiplied by weight into y_dtype (the
+ * promotion of x_dtype and w_dtype). Only y is written.
+ * Replaces the GPU branch of rmsnorm_residual_fused (normalization.py:
+ * 219-255 -> _rmsnorm_residual_triton :162-183 -> _rmsnorm_residual_kernel
+ * :103-139).
+ */
+int ra_rmsnorm_residual(const void *x, int64_t ldx, int x_dtype,
+                        const void *residual, int64_t ldr, int r_dtype,
+                        const void *weight, int w_dtype,
+                        void *y, int64_t ldy, int y_dtype,
+                        int64_t rows, int64_t hidden, float eps, void *stream);
 
 /*
  * out[i] = silu(gate[i]) * up[i] over n contiguous elements, fp32 math, one

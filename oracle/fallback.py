@@ -9,6 +9,8 @@ uses the same ops, on CPU tensors only:
                    = (q.float() * s[:, None]).to(dtype)
   rmsnorm_torch    src/rotalabs_accel/kernels/normalization.py:32-45
                    = (x.float() * rsqrt(mean(x.float()^2, -1) + eps)).to(x.dtype) * w
+  rmsnorm_residual_torch  normalization.py:48-64
+                   = the same on v = (x + residual).float(), rounded to x.dtype
   swiglu_torch     src/rotalabs_accel/kernels/activations.py:36-45
                    = silu(gate) * up
 
@@ -42,6 +44,13 @@ def rmsnorm_ref(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Te
     xf = x.float()
     r = torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
     return (xf * r).to(x.dtype) * w
+
+
+def rmsnorm_residual_ref(x: torch.Tensor, r: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """normalization.py:48-64 on CPU tensors."""
+    v = (x + r).float()
+    rr = torch.rsqrt(v.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return (v * rr).to(x.dtype) * w
 
 
 def swiglu_ref(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:

@@ -163,8 +163,21 @@ int ra_rmsnorm(const void *x, int64_t ldx, int x_dtype, const void *weight, int 
   if (y_dtype != promoted) return RA_ERR_DTYPE;
   if (rows == 0 || hidden == 0) return RA_OK;
   if (!x || !weight || !y || ldx < hidden || ldy < hidden) return RA_ERR_ARG;
-  return to_status(rmsnorm_launch(x, ldx, x_dtype, weight, w_dtype, y, ldy, y_dtype, rows, hidden, eps,
-                                  static_cast<hipStream_t>(stream)));
+  return to_status(rmsnorm_launch(x, ldx, x_dtype, nullptr, 0, x_dtype, weight, w_dtype, y, ldy, y_dtype, rows,
+                                  hidden, eps, static_cast<hipStream_t>(stream)));
+}
+
+int ra_rmsnorm_residual(const void *x, int64_t ldx, int x_dtype, const void *residual, int64_t ldr, int r_dtype,
+                        const void *weight, int w_dtype, void *y, int64_t ldy, int y_dtype, int64_t rows,
+                        int64_t hidden, float eps, void *stream) {
+  if (rows < 0 || hidden < 0 || rows > INT32_MAX || hidden > INT32_MAX) return RA_ERR_ARG;
+  if (!valid_act(x_dtype) || !valid_act(r_dtype) || !valid_act(w_dtype) || !valid_act(y_dtype)) return RA_ERR_DTYPE;
+  const int promoted = x_dtype == w_dtype ? x_dtype : RA_F32;
+  if (y_dtype != promoted) return RA_ERR_DTYPE;
+  if (rows == 0 || hidden == 0) return RA_OK;
+  if (!x || !residual || !weight || !y || ldx < hidden || ldr < hidden || ldy < hidden) return RA_ERR_ARG;
+  return to_status(rmsnorm_launch(x, ldx, x_dtype, residual, ldr, r_dtype, weight, w_dtype, y, ldy, y_dtype, rows,
+                                  hidden, eps, static_cast<hipStream_t>(stream)));
 }
 
 int ra_swiglu(const void *gate, const void *up, void *out, int64_t n, int dtype, void *stream) {

@@ -75,9 +75,9 @@ hipError_t gemv_launch(const GemmArgs &a, hipStream_t s);
 bool gateup_gemv_supported(const GateUpArgs &a);
 hipError_t gateup_gemv_launch(const GateUpArgs &a, hipStream_t s);
 
-hipError_t rmsnorm_launch(const void *x, int64_t ldx, int x_dt, const void *w, int w_dt, void *y,
-                          int64_t ldy, int y_dt, int64_t rows, int64_t hidden, float eps,
-                          hipStream_t s);
+hipError_t rmsnorm_launch(const void *x, int64_t ldx, int x_dt, const void *r, int64_t ldr, int r_dt,
+                          const void *w, int w_dt, void *y, int64_t ldy, int y_dt, int64_t rows, int64_t hidden,
+                          float eps, hipStream_t s);
 hipError_t swiglu_launch(const void *g, const void *u, void *o, int64_t n, int dt, hipStream_t s);
 hipError_t quantize_launch(const void *w, int64_t ldw, int w_dt, int64_t N, int64_t K, int8_t *q,
                            int64_t ldq, float *scale, hipStream_t s);

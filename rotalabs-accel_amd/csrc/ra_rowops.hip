@@ -23,36 +23,47 @@ __device__ __forceinline__ float block_reduce(float v, float *smem) {
   return r;
 }
 
-// y = round_y( round_x(x * rsqrt(mean(x^2) + eps)) * w ), as rmsnorm_torch
-// (src/rotalabs_accel/kernels/normalization.py:43-45): the normalised value
-// is stored in x's dtype, then multiplied by the weight in the promoted dtype.
+// y = round_y( round_x(v * rsqrt(mean(v^2) + eps)) * w ) with v = x, as
+// rmsnorm_torch (src/rotalabs_accel/kernels/normalization.py:43-45): the
+// normalised value is stored in x's dtype, then multiplied by the weight in
+// the promoted dtype. With a residual r, v = round_s(x + r) in s, the
+// promotion of x's and r's dtypes, as rmsnorm_residual_torch (:60-62)
+// computes (x + residual) before .float().
 // rsqrt is 1/sqrt with both operations correctly rounded (no approximation).
 __global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(const void *__restrict__ x, int64_t ldx,
-                                                              int x_dt, const void *__restrict__ w,
+                                                              int x_dt, const void *__restrict__ r,
+                                                              int64_t ldr, int r_dt, int s_dt,
+                                                              const void *__restrict__ w,
                                                               int w_dt, void *__restrict__ y,
                                                               int64_t ldy, int y_dt, int hidden,
                                                               float eps) {
   __shared__ float smem[kRowThreads / 64];
   const int64_t row = blockIdx.x;
+  auto in = [&](int i) -> float {
+    const float v = load_as_f32(x, row * ldx + i, x_dt);
+    return r ? round_through(v + load_as_f32(r, row * ldr + i, r_dt), s_dt) : v;
+  };
   float ss = 0.f;
   for (int i = threadIdx.x; i < hidden; i += kRowThreads) {
-    const float v = load_as_f32(x, row * ldx + i, x_dt);
+    const float v = in(i);
     ss += v * v;
   }
   const float total = block_reduce<false>(ss, smem);
-  const float r = 1.0f / sqrtf(total / (float)hidden + eps);
+  const float rr = 1.0f / sqrtf(total / (float)hidden + eps);
   for (int i = threadIdx.x; i < hidden; i += kRowThreads) {
-    const float v = round_through(load_as_f32(x, row * ldx + i, x_dt) * r, x_dt);
+    const float v = round_through(in(i) * rr, x_dt);
     store_from_f32(y, row * ldy + i, y_dt, v * load_as_f32(w, i, w_dt));
   }
 }
 
-// Same arithmetic for x, w, y of one 16-bit dtype with hidden % 8 == 0: every
-// thread loads its VPT 16-byte chunks of the row (and of w) at once, keeps them
-// in registers for the normalisation, and stores 16-byte chunks -- one pass
-// over memory with all loads in flight, instead of a latency-bound loop.
-template <int DT, int VPT>
+// Same arithmetic for x, (r,) w, y of one 16-bit dtype with hidden % 8 == 0:
+// every thread loads its VPT 16-byte chunks of the row (and of r and w) at
+// once, keeps them in registers for the normalisation, and stores 16-byte
+// chunks -- one pass over memory with all loads in flight, instead of a
+// latency-bound loop.
+template <int DT, int VPT, bool RES>
 __global__ __launch_bounds__(kRowThreads) void rmsnorm_vec_kernel(const uint16_t *__restrict__ x, int64_t ldx,
+                                                                  const uint16_t *__restrict__ r, int64_t ldr,
                                                                   const uint16_t *__restrict__ w,
                                                                   uint16_t *__restrict__ y, int64_t ldy,
                                                                   int hidden, float eps) {
@@ -61,71 +72,82 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_vec_kernel(const uint16_t
   const int64_t row = blockIdx.x;
   const int nch = hidden / 8;
   const uint16_t *xr = x + row * ldx;
-  uint4 xv[VPT], wv[VPT];
+  uint4 xv[VPT], rv[VPT], wv[VPT];
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     const int c = min((int)threadIdx.x + kRowThreads * j, nch - 1);  // clamped: loads stay unconditional
     xv[j] = *reinterpret_cast<const uint4 *>(xr + 8 * c);
+    if (RES) rv[j] = *reinterpret_cast<const uint4 *>(r + row * ldr + 8 * c);
     wv[j] = *reinterpret_cast<const uint4 *>(w + 8 * c);
   }
+  // v = x (+ r, rounded to the dtype)
+  float v[VPT][8];
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
-    if ((int)threadIdx.x + kRowThreads * j >= nch) continue;
     const uint16_t *h = reinterpret_cast<const uint16_t *>(&xv[j]);
+    const uint16_t *hr = reinterpret_cast<const uint16_t *>(&rv[j]);
+    const bool live = (int)threadIdx.x + kRowThreads * j < nch;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float v = A::in(h[e]);
-      ss += v * v;
+      v[j][e] = RES ? A::rnd(A::in(h[e]) + A::in(hr[e])) : A::in(h[e]);
+      if (live) ss += v[j][e] * v[j][e];
     }
   }
   const float total = block_reduce<false>(ss, smem);
-  const float r = 1.0f / sqrtf(total / (float)hidden + eps);
+  const float rr = 1.0f / sqrtf(total / (float)hidden + eps);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     const int c = (int)threadIdx.x + kRowThreads * j;
     if (c >= nch) continue;
-    const uint16_t *h = reinterpret_cast<const uint16_t *>(&xv[j]);
     const uint16_t *hw = reinterpret_cast<const uint16_t *>(&wv[j]);
     uint4 o;
     uint16_t *ho = reinterpret_cast<uint16_t *>(&o);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ho[e] = A::out(A::rnd(A::in(h[e]) * r) * A::in(hw[e]));
+    for (int e = 0; e < 8; ++e) ho[e] = A::out(A::rnd(v[j][e] * rr) * A::in(hw[e]));
     *reinterpret_cast<uint4 *>(y + row * ldy + 8 * c) = o;
   }
 }
 
-template <int DT>
-static void rmsnorm_vec_launch(const void *x, int64_t ldx, const void *w, void *y, int64_t ldy, int64_t rows,
-                               int hidden, float eps, hipStream_t s) {
+template <int DT, bool RES>
+static void rmsnorm_vec_launch(const void *x, int64_t ldx, const void *r, int64_t ldr, const void *w, void *y,
+                               int64_t ldy, int64_t rows, int hidden, float eps, hipStream_t s) {
   const int nch = hidden / 8;
-  const uint16_t *xp = static_cast<const uint16_t *>(x), *wp = static_cast<const uint16_t *>(w);
+  const uint16_t *xp = static_cast<const uint16_t *>(x), *rp = static_cast<const uint16_t *>(r),
+                 *wp = static_cast<const uint16_t *>(w);
   uint16_t *yp = static_cast<uint16_t *>(y);
   const dim3 grid((unsigned)rows), block(kRowThreads);
   if (nch <= kRowThreads)
-    hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 1>), grid, block, 0, s, xp, ldx, wp, yp, ldy, hidden, eps);
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 1, RES>), grid, block, 0, s, xp, ldx, rp, ldr, wp, yp, ldy, hidden, eps);
   else if (nch <= 2 * kRowThreads)
-    hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 2>), grid, block, 0, s, xp, ldx, wp, yp, ldy, hidden, eps);
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 2, RES>), grid, block, 0, s, xp, ldx, rp, ldr, wp, yp, ldy, hidden, eps);
   else if (nch <= 4 * kRowThreads)
-    hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 4>), grid, block, 0, s, xp, ldx, wp, yp, ldy, hidden, eps);
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 4, RES>), grid, block, 0, s, xp, ldx, rp, ldr, wp, yp, ldy, hidden, eps);
   else
-    hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 8>), grid, block, 0, s, xp, ldx, wp, yp, ldy, hidden, eps);
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<DT, 8, RES>), grid, block, 0, s, xp, ldx, rp, ldr, wp, yp, ldy, hidden, eps);
 }
 
-hipError_t rmsnorm_launch(const void *x, int64_t ldx, int x_dt, const void *w, int w_dt, void *y,
-                          int64_t ldy, int y_dt, int64_t rows, int64_t hidden, float eps,
-                          hipStream_t s) {
-  const bool vec = (x_dt == RA_F16 || x_dt == RA_BF16) && w_dt == x_dt && y_dt == x_dt && hidden % 8 == 0 &&
-                   hidden >= 8 && hidden <= 8 * 8 * kRowThreads && ldx % 8 == 0 && ldy % 8 == 0 &&
-                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
-                     reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+hipError_t rmsnorm_launch(const void *x, int64_t ldx, int x_dt, const void *r, int64_t ldr, int r_dt,
+                          const void *w, int w_dt, void *y, int64_t ldy, int y_dt, int64_t rows, int64_t hidden,
+                          float eps, hipStream_t s) {
+  const bool vec = (x_dt == RA_F16 || x_dt == RA_BF16) && w_dt == x_dt && y_dt == x_dt && (!r || r_dt == x_dt) &&
+                   hidden % 8 == 0 && hidden >= 8 && hidden <= 8 * 8 * kRowThreads && ldx % 8 == 0 &&
+                   ldy % 8 == 0 && (!r || ldr % 8 == 0) &&
+                   ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(r) |
+                     reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(y)) & 15) == 0;
   if (vec) {
-    if (x_dt == RA_F16) rmsnorm_vec_launch<RA_F16>(x, ldx, w, y, ldy, rows, (int)hidden, eps, s);
-    else rmsnorm_vec_launch<RA_BF16>(x, ldx, w, y, ldy, rows, (int)hidden, eps, s);
+    if (x_dt == RA_F16) {
+      if (r) rmsnorm_vec_launch<RA_F16, true>(x, ldx, r, ldr, w, y, ldy, rows, (int)hidden, eps, s);
+      else rmsnorm_vec_launch<RA_F16, false>(x, ldx, r, ldr, w, y, ldy, rows, (int)hidden, eps, s);
+    } else {
+      if (r) rmsnorm_vec_launch<RA_BF16, true>(x, ldx, r, ldr, w, y, ldy, rows, (int)hidden, eps, s);
+      else rmsnorm_vec_launch<RA_BF16, false>(x, ldx, r, ldr, w, y, ldy, rows, (int)hidden, eps, s);
+    }
     return hipGetLastError();
   }
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kRowThreads), 0, s, x, ldx, x_dt, w, w_dt,
-                     y, ldy, y_dt, (int)hidden, eps);
+  const int s_dt = !r ? x_dt : (x_dt == r_dt ? x_dt : RA_F32);  // dtype of x + r
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kRowThreads), 0, s, x, ldx, x_dt, r, ldr, r_dt,
+                     s_dt, w, w_dt, y, ldy, y_dt, (int)hidden, eps);
   return hipGetLastError();
 }
 

@@ -18,6 +18,8 @@ from rotalabs_accel.kernels import (
     int8_gemm_torch,
     int8_mlp,
     rmsnorm,
+    rmsnorm_residual_fused,
+    rmsnorm_residual_torch,
     rmsnorm_torch,
     swiglu_fused,
     swiglu_torch,
@@ -35,6 +37,8 @@ __all__ = [
     "HAS_HIP",
     "rmsnorm",
     "rmsnorm_torch",
+    "rmsnorm_residual_fused",
+    "rmsnorm_residual_torch",
     "TritonRMSNorm",
     "swiglu_fused",
     "swiglu_torch",

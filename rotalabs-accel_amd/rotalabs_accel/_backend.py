@@ -20,7 +20,7 @@ _lock = threading.Lock()
 _lib = None
 _load_error: str | None = None
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # enum ra_dtype
 F16, BF16, F32 = 0, 1, 2
@@ -44,6 +44,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "ra_w8a16_gemm_select": ([i64, i64, i64, i32], i32),
         "ra_w8a16_gateup_swiglu": ([p, i64, i32, p, i64, p, p, i64, i64, i64, i64, p], i32),
         "ra_rmsnorm": ([p, i64, i32, p, i32, p, i64, i32, i64, i64, f32, p], i32),
+        "ra_rmsnorm_residual": ([p, i64, i32, p, i64, i32, p, i32, p, i64, i32, i64, i64, f32, p], i32),
         "ra_swiglu": ([p, p, p, i64, i32, p], i32),
         "ra_quantize_per_channel": ([p, i64, i32, i64, i64, p, i64, p, p], i32),
     }
@@ -65,7 +66,7 @@ def load():
         try:
             lib = ctypes.CDLL(path)
             _declare(lib)
-        except OSError as e:
+        except (OSError, AttributeError) as e:  # AttributeError: a symbol of this ABI is missing
             _load_error = f"cannot load {path}: {e}"
             raise RuntimeError(
                 f"rotalabs_accel: the HIP library is required for GPU tensors but {_load_error}. "

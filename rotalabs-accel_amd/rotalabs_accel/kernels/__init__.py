@@ -7,7 +7,13 @@ from rotalabs_accel._backend import available as _hip_available
 from rotalabs_accel.kernels.activations import swiglu_fused, swiglu_torch
 from rotalabs_accel.kernels.gemm import Int8Linear, int8_gemm, int8_gemm_torch
 from rotalabs_accel.kernels.mlp import Int8SwiGLUMLP, int8_gateup_swiglu, int8_mlp
-from rotalabs_accel.kernels.normalization import TritonRMSNorm, rmsnorm, rmsnorm_torch
+from rotalabs_accel.kernels.normalization import (
+    TritonRMSNorm,
+    rmsnorm,
+    rmsnorm_residual_fused,
+    rmsnorm_residual_torch,
+    rmsnorm_torch,
+)
 
 HAS_TRITON = False
 HAS_HIP = _hip_available()
@@ -17,6 +23,8 @@ __all__ = [
     "HAS_HIP",
     "rmsnorm",
     "rmsnorm_torch",
+    "rmsnorm_residual_fused",
+    "rmsnorm_residual_torch",
     "TritonRMSNorm",
     "swiglu_fused",
     "swiglu_torch",

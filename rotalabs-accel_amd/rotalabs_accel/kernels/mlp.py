@@ -10,11 +10,12 @@ to the fp32 accumulators in the epilogue, so gate and up are never written
 to memory:
 
     h = rmsnorm(x, norm_weight, eps)                       ra_rmsnorm
+        (or rmsnorm_residual_fused(x, residual, ...)      ra_rmsnorm_residual)
     a = silu(h @ Wg^T * sg) * (h @ Wu^T * su)              ra_w8a16_gateup_swiglu
     y = a @ Wd^T * sd                                      ra_w8a16_gemm
 
 On CPU tensors the same composition runs with the PyTorch ops
-(rmsnorm_torch, int8_gemm_torch, swiglu_torch).
+(rmsnorm_torch / rmsnorm_residual_torch, int8_gemm_torch, swiglu_torch).
 """
 from __future__ import annotations
 
@@ -25,7 +26,7 @@ import torch
 from rotalabs_accel import _backend
 from rotalabs_accel.kernels.activations import swiglu_torch
 from rotalabs_accel.kernels.gemm import _rows, int8_gemm, int8_gemm_torch
-from rotalabs_accel.kernels.normalization import rmsnorm
+from rotalabs_accel.kernels.normalization import rmsnorm, rmsnorm_residual_fused
 from rotalabs_accel.quantization.symmetric import quantize_weight_per_channel
 
 
@@ -63,9 +64,13 @@ def int8_gateup_swiglu(x: torch.Tensor, weight_gate_up: torch.Tensor, scale_gate
 
 def int8_mlp(x: torch.Tensor, norm_weight: torch.Tensor, weight_gate_up: torch.Tensor,
              scale_gate_up: torch.Tensor, weight_down: torch.Tensor, scale_down: torch.Tensor,
-             eps: float = 1e-6) -> torch.Tensor:
-    """RMSNorm -> fused gate/up + SwiGLU -> down projection."""
-    h = rmsnorm(x, norm_weight, eps)
+             eps: float = 1e-6, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """RMSNorm (of ``x + residual`` when given) -> fused gate/up + SwiGLU ->
+    down projection."""
+    if residual is not None:
+        h = rmsnorm_residual_fused(x, residual, norm_weight, eps)
+    else:
+        h = rmsnorm(x, norm_weight, eps)
     a = int8_gateup_swiglu(h, weight_gate_up, scale_gate_up)
     return int8_gemm(a, weight_down, scale_down)
 
@@ -127,11 +132,13 @@ class Int8SwiGLUMLP(torch.nn.Module):
             module.norm_weight.data.copy_(norm_weight)
         return module
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """MLP of ``rmsnorm(x)``, or of ``rmsnorm(x + residual)`` (one fused
+        pass) when the residual stream is given."""
         if not self._quantized:
             raise RuntimeError("Weights not quantized. Call quantize_weights() first.")
         return int8_mlp(x, self.norm_weight, self.weight_gate_up, self.scale_gate_up,
-                        self.weight_down, self.scale_down, self.eps)
+                        self.weight_down, self.scale_down, self.eps, residual)
 
     def extra_repr(self) -> str:
         return (f"hidden_size={self.hidden_size}, intermediate_size={self.intermediate_size}, "

@@ -65,6 +65,27 @@ def test_rmsnorm_module():
 
 
 # ---- bit-level agreement with the oracle / golden vectors --------------------
+def test_rmsnorm_residual_cpu_path():
+    """CPU tensors take rmsnorm_residual_torch (the reference's fallback):
+    the oracle's bits, the reference's asserts, and the MLP composition with a
+    residual stream equals the one on the rounded sum."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(3, 5, 64, generator=g).to(torch.bfloat16)
+    r = torch.randn(3, 5, 64, generator=g).to(torch.bfloat16)
+    w = (1 + 0.01 * torch.randn(64, generator=g)).to(torch.bfloat16)
+    y = ra.rmsnorm_residual_fused(x, r, w)
+    assert y.shape == x.shape and torch.equal(y, fallback.rmsnorm_residual_ref(x, r, w))
+    assert torch.equal(ra.rmsnorm_residual_torch(x, r, w), y)
+    with pytest.raises(AssertionError, match="Shape mismatch"):
+        ra.rmsnorm_residual_fused(x, r[:, :4], w)
+    with pytest.raises(AssertionError, match="Hidden dim mismatch"):
+        ra.rmsnorm_residual_fused(x, r, w[:32])
+    mlp = ra.Int8SwiGLUMLP(64, 96)
+    mlp.quantize_weights(torch.randn(96, 64, generator=g) * 0.02, torch.randn(96, 64, generator=g) * 0.02,
+                         torch.randn(64, 96, generator=g) * 0.02)
+    assert torch.equal(mlp(x, r), mlp(x + r))
+
+
 def test_quantize_fp32_bit_exact():
     g = torch.Generator().manual_seed(11)
     w = torch.randn(96, 257, generator=g) * 0.02

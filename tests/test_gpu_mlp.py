@@ -84,6 +84,47 @@ def test_rmsnorm_widths(gpu, rows, hidden):
     assert (y == ref).float().mean() > 0.99
 
 
+@pytest.mark.parametrize("xdt,rdt,wdt", [(torch.bfloat16, torch.bfloat16, torch.bfloat16),
+                                         (torch.float16, torch.float16, torch.float16),
+                                         (torch.float16, torch.float32, torch.float32),
+                                         (torch.bfloat16, torch.float32, torch.bfloat16)])
+@pytest.mark.parametrize("rows,hidden", [(33, 8192), (5, 40), (2, 16392)])
+def test_rmsnorm_residual_vs_oracle(gpu, xdt, rdt, wdt, rows, hidden):
+    """ra_rmsnorm_residual (single-pass and general kernels) against the
+    restated fallback: all but a sliver of 16-bit outputs bit-identical."""
+    g = torch.Generator().manual_seed(rows + hidden)
+    x = (torch.randn(rows, hidden, generator=g) * 2).to(xdt)
+    r = (torch.randn(rows, hidden, generator=g) * 2).to(rdt)
+    w = (1 + 0.01 * torch.randn(hidden, generator=g)).to(wdt)
+    print(f"  rmsnorm_residual {rows}x{hidden} {xdt} {rdt} {wdt}", flush=True)
+    y = ra.rmsnorm_residual_fused(x.to(gpu), r.to(gpu), w.to(gpu), 1e-6).cpu()
+    ref = fallback.rmsnorm_residual_ref(x, r, w, 1e-6)
+    assert y.dtype == ref.dtype and y.shape == ref.shape
+    torch.testing.assert_close(y.float(), ref.float(), rtol=1e-2, atol=1e-2)
+    if y.dtype != torch.float32:
+        assert (y == ref).float().mean() > 0.99
+
+
+def test_rmsnorm_residual_layouts_and_mlp(gpu):
+    """Leading dims, a strided residual, and the MLP block with a residual
+    stream (equal to the block on the rounded sum)."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 7, 4096, generator=g).to(torch.bfloat16)
+    rb = torch.randn(2, 7, 4104, generator=g).to(torch.bfloat16)
+    r = rb[..., 8:]                                      # row stride 4104
+    w = (1 + 0.01 * torch.randn(4096, generator=g)).to(torch.bfloat16)
+    y = ra.rmsnorm_residual_fused(x.to(gpu), rb.to(gpu)[..., 8:], w.to(gpu)).cpu()
+    ref = fallback.rmsnorm_residual_ref(x, r, w)
+    assert (y == ref).float().mean() > 0.99
+    mlp = ra.Int8SwiGLUMLP(4096, 1024)
+    mlp.quantize_weights(torch.randn(1024, 4096, generator=g) * 0.02, torch.randn(1024, 4096, generator=g) * 0.02,
+                         torch.randn(4096, 1024, generator=g) * 0.02)
+    mlp = mlp.to(gpu)
+    a = mlp(x.to(gpu), r.to(gpu)).cpu()
+    b = mlp((x + r).to(gpu)).cpu()
+    assert torch.equal(a, b)
+
+
 def test_rmsnorm_golden(gpu, golden):
     x = _t16(golden["rms_x_bf16"], torch.bfloat16)
     w = _t16(golden["rms_w_bf16"], torch.bfloat16)

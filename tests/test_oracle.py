@@ -189,3 +189,28 @@ def test_dequantize_closed_form():
     assert np.array_equal(ref.float().numpy(), mine)
     refb = fallback.dequantize_ref(torch.from_numpy(q), torch.from_numpy(s), torch.bfloat16)
     assert np.array_equal(refb.float().numpy(), oq.dequantize(q, s, "bf16"))
+
+
+def test_rmsnorm_residual_oracle_pinned(golden):
+    """rmsnorm_residual_ref (normalization.py:48-64) pinned by identities:
+    a zero residual is rmsnorm of x; with equal dtypes it is rmsnorm of the
+    rounded sum (so a dropped or mis-signed residual term, or a rounding to
+    the wrong dtype, fails); mixed dtypes round the sum in the promoted type
+    and the normalised value in x's dtype (float64 closed form, 1 ulp)."""
+    x = _t16(golden["rms_x_bf16"], torch.bfloat16)
+    w = _t16(golden["rms_w_bf16"], torch.bfloat16)
+    ref = _t16(golden["rms_y_bf16"], torch.bfloat16)
+    assert torch.equal(fallback.rmsnorm_residual_ref(x, torch.zeros_like(x), w), ref)
+    g = torch.Generator().manual_seed(3)
+    r = (torch.randn(x.shape, generator=g) * 0.5).to(torch.bfloat16)
+    assert torch.equal(fallback.rmsnorm_residual_ref(x, r, w), fallback.rmsnorm_ref(x + r, w))
+    assert not torch.equal(fallback.rmsnorm_residual_ref(x, r, w), fallback.rmsnorm_ref(x - r, w))
+    # fp16 x + fp32 residual: the sum stays fp32, the normalised value is fp16
+    xh = (torch.randn(4, 96, generator=g) * 2).half()
+    rf = torch.randn(4, 96, generator=g) * 0.25
+    wf = 1 + 0.01 * torch.randn(96, generator=g)
+    y = fallback.rmsnorm_residual_ref(xh, rf, wf)
+    assert y.dtype == torch.float32
+    v = xh.double() + rf.double()
+    n = (v / torch.sqrt((v * v).mean(dim=-1, keepdim=True) + 1e-6)).half().double() * wf.double()
+    assert torch.allclose(y.double(), n, rtol=2 ** -10, atol=1e-6)
