@@ -58,6 +58,16 @@ def swiglu_ref(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     return F.silu(gate) * up
 
 
+def swiglu_ffn_ref(x, q_gu, s_gu, q_down, s_down, b_gu=None, b_down=None):
+    """The reference SwiGLU module's forward (activations.py:175-178) with
+    int8 projections: down(silu(gate(x)) * up(x)), gate/up as one [2I,H]
+    weight."""
+    inter = q_gu.shape[0] // 2
+    gu = int8_gemm_ref(x, q_gu, s_gu, b_gu)
+    a = swiglu_ref(gu[..., :inter], gu[..., inter:])
+    return int8_gemm_ref(a, q_down, s_down, b_down)
+
+
 def mlp_ref(x, norm_w, q_gu, s_gu, q_down, s_down, eps: float = 1e-6):
     """RMSNorm -> Int8 gate+up (one [2I,H] weight) -> SwiGLU -> Int8 down."""
     inter = q_gu.shape[0] // 2

@@ -11,7 +11,9 @@ from rotalabs_accel._version import __version__
 from rotalabs_accel.kernels import (
     HAS_HIP,
     Int8Linear,
+    Int8SwiGLU,
     Int8SwiGLUMLP,
+    SwiGLU,
     TritonRMSNorm,
     int8_gateup_swiglu,
     int8_gemm,
@@ -42,6 +44,8 @@ __all__ = [
     "TritonRMSNorm",
     "swiglu_fused",
     "swiglu_torch",
+    "SwiGLU",
+    "Int8SwiGLU",
     "int8_gemm",
     "int8_gemm_torch",
     "Int8Linear",

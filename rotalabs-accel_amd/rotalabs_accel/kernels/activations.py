@@ -33,3 +33,27 @@ def swiglu_fused(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
                                          _backend.dtype_code(g.dtype), _backend.stream_handle(g.device)))
         return out
     return swiglu_torch(gate, up)
+
+
+class SwiGLU(torch.nn.Module):
+    """SwiGLU FFN ``w_down(silu(w_gate(x)) * w_up(x))`` with nn.Linear
+    projections -- the reference's module (activations.py:141-181), same
+    constructor, parameters and forward; the activation runs ``swiglu_fused``
+    (the HIP kernel on GPU tensors). ``Int8SwiGLU.from_swiglu`` turns it into
+    the int8 FFN."""
+
+    def __init__(self, hidden_size: int, intermediate_size: int, bias: bool = False):
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.intermediate_size = intermediate_size
+        self.w_gate = torch.nn.Linear(hidden_size, intermediate_size, bias=bias)
+        self.w_up = torch.nn.Linear(hidden_size, intermediate_size, bias=bias)
+        self.w_down = torch.nn.Linear(intermediate_size, hidden_size, bias=bias)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        gate = self.w_gate(x)
+        up = self.w_up(x)
+        return self.w_down(swiglu_fused(gate, up))
+
+    def extra_repr(self) -> str:
+        return f"hidden_size={self.hidden_size}, intermediate_size={self.intermediate_size}"

@@ -24,7 +24,7 @@ from typing import Optional
 import torch
 
 from rotalabs_accel import _backend
-from rotalabs_accel.kernels.activations import swiglu_torch
+from rotalabs_accel.kernels.activations import SwiGLU, swiglu_fused, swiglu_torch
 from rotalabs_accel.kernels.gemm import _rows, int8_gemm, int8_gemm_torch
 from rotalabs_accel.kernels.normalization import rmsnorm, rmsnorm_residual_fused
 from rotalabs_accel.quantization.symmetric import quantize_weight_per_channel
@@ -143,3 +143,81 @@ class Int8SwiGLUMLP(torch.nn.Module):
     def extra_repr(self) -> str:
         return (f"hidden_size={self.hidden_size}, intermediate_size={self.intermediate_size}, "
                 f"eps={self.eps}, quantized={self._quantized}")
+
+
+class Int8SwiGLU(torch.nn.Module):
+    """The reference's SwiGLU FFN (activations.py:141-181:
+    ``w_down(silu(w_gate(x)) * w_up(x))``) with W8A16 int8 projections.
+
+    Same constructor as the reference module. Buffers: ``weight_gate_up``
+    int8 [2I, H] (= [Wg; Wu], per-row scales, so identical to quantizing the
+    two projections separately), ``scale_gate_up`` fp32 [2I], ``weight_down``
+    int8 [H, I], ``scale_down`` fp32 [H]; with ``bias=True`` fp16 parameters
+    ``bias_gate_up`` [2I] and ``bias_down`` [H] (fp16 like ``Int8Linear``'s).
+    Without biases the gate and up projections run as one GEMM with SwiGLU in
+    its epilogue (``int8_gateup_swiglu``); with biases they run as one biased
+    GEMM, then ``swiglu_fused``. CPU tensors run the same composition with the
+    PyTorch ops.
+    """
+
+    def __init__(self, hidden_size: int, intermediate_size: int, bias: bool = False):
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.intermediate_size = intermediate_size
+        self.register_buffer("weight_gate_up",
+                             torch.zeros(2 * intermediate_size, hidden_size, dtype=torch.int8))
+        self.register_buffer("scale_gate_up", torch.ones(2 * intermediate_size, dtype=torch.float32))
+        self.register_buffer("weight_down", torch.zeros(hidden_size, intermediate_size, dtype=torch.int8))
+        self.register_buffer("scale_down", torch.ones(hidden_size, dtype=torch.float32))
+        if bias:
+            self.bias_gate_up = torch.nn.Parameter(torch.zeros(2 * intermediate_size, dtype=torch.float16))
+            self.bias_down = torch.nn.Parameter(torch.zeros(hidden_size, dtype=torch.float16))
+        else:
+            self.register_parameter("bias_gate_up", None)
+            self.register_parameter("bias_down", None)
+        self._quantized = False
+
+    def quantize_weights(self, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor) -> None:
+        """Per-output-channel quantization of the projection weights
+        ([I, H], [I, H], [H, I]), on the CPU like ``Int8Linear.quantize_weights``."""
+        H, inter = self.hidden_size, self.intermediate_size
+        assert w_gate.shape == (inter, H) and w_up.shape == (inter, H) and w_down.shape == (H, inter)
+        dev = self.weight_gate_up.device
+        qg, sg = quantize_weight_per_channel(w_gate.detach().cpu())
+        qu, su = quantize_weight_per_channel(w_up.detach().cpu())
+        qd, sd = quantize_weight_per_channel(w_down.detach().cpu())
+        self.weight_gate_up[:inter].copy_(qg.to(dev))
+        self.weight_gate_up[inter:].copy_(qu.to(dev))
+        self.scale_gate_up[:inter].copy_(sg.to(dev))
+        self.scale_gate_up[inter:].copy_(su.to(dev))
+        self.weight_down.copy_(qd.to(dev))
+        self.scale_down.copy_(sd.to(dev))
+        self._quantized = True
+
+    @classmethod
+    def from_swiglu(cls, module: SwiGLU) -> "Int8SwiGLU":
+        """Quantize a ``SwiGLU`` FFN (on the device of its weights)."""
+        has_bias = module.w_gate.bias is not None
+        out = cls(module.hidden_size, module.intermediate_size, bias=has_bias).to(module.w_gate.weight.device)
+        out.quantize_weights(module.w_gate.weight.data, module.w_up.weight.data, module.w_down.weight.data)
+        if has_bias:
+            inter = module.intermediate_size
+            out.bias_gate_up.data[:inter].copy_(module.w_gate.bias.data.half())
+            out.bias_gate_up.data[inter:].copy_(module.w_up.bias.data.half())
+            out.bias_down.data.copy_(module.w_down.bias.data.half())
+        return out
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if not self._quantized:
+            raise RuntimeError("Weights not quantized. Call quantize_weights() first.")
+        inter = self.intermediate_size
+        if self.bias_gate_up is None:
+            a = int8_gateup_swiglu(x, self.weight_gate_up, self.scale_gate_up)
+        else:
+            gu = int8_gemm(x, self.weight_gate_up, self.scale_gate_up, self.bias_gate_up)
+            a = swiglu_fused(gu[..., :inter].contiguous(), gu[..., inter:].contiguous())
+        return int8_gemm(a, self.weight_down, self.scale_down, self.bias_down)
+
+    def extra_repr(self) -> str:
+        return (f"hidden_size={self.hidden_size}, intermediate_size={self.intermediate_size}, "
+                f"bias={self.bias_down is not None}, quantized={self._quantized}")

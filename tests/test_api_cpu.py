@@ -86,6 +86,31 @@ def test_rmsnorm_residual_cpu_path():
     assert torch.equal(mlp(x, r), mlp(x + r))
 
 
+@pytest.mark.parametrize("bias", [False, True])
+def test_swiglu_modules_cpu(bias):
+    """SwiGLU keeps the reference module's structure; Int8SwiGLU.from_swiglu
+    quantizes it and its CPU forward is the oracle's int8 FFN composition."""
+    g = torch.Generator().manual_seed(13)
+    torch.manual_seed(13)
+    m = ra.SwiGLU(64, 96, bias=bias)
+    assert [n for n, _ in m.named_parameters()] == (
+        ["w_gate.weight", "w_gate.bias", "w_up.weight", "w_up.bias", "w_down.weight", "w_down.bias"] if bias
+        else ["w_gate.weight", "w_up.weight", "w_down.weight"])
+    x = torch.randn(3, 64, generator=g)
+    ref = m.w_down(torch.nn.functional.silu(m.w_gate(x)) * m.w_up(x))
+    assert torch.allclose(m(x), ref)
+    q = ra.Int8SwiGLU.from_swiglu(m)
+    xh = x.half()
+    y = q(xh)
+    want = fallback.swiglu_ffn_ref(xh, q.weight_gate_up, q.scale_gate_up, q.weight_down, q.scale_down,
+                                   q.bias_gate_up, q.bias_down)
+    assert y.dtype == torch.float16 and torch.equal(y, want)
+    qg, _ = ra.quantize_weight_per_channel(m.w_gate.weight.data)
+    assert torch.equal(q.weight_gate_up[:96], qg)
+    with pytest.raises(RuntimeError, match="not quantized"):
+        ra.Int8SwiGLU(64, 96)(xh)
+
+
 def test_quantize_fp32_bit_exact():
     g = torch.Generator().manual_seed(11)
     w = torch.randn(96, 257, generator=g) * 0.02

@@ -125,6 +125,26 @@ def test_rmsnorm_residual_layouts_and_mlp(gpu):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("M", [1, 17, 300])
+def test_int8_swiglu_module_vs_oracle(gpu, M, bias):
+    """Int8SwiGLU on the GPU (fused gate/up + SwiGLU epilogue, or the biased
+    GEMM + swiglu_fused) against the oracle's int8 FFN composition."""
+    torch.manual_seed(M)
+    m = ra.SwiGLU(1024, 1536, bias=bias)
+    q = ra.Int8SwiGLU.from_swiglu(m)
+    g = torch.Generator().manual_seed(M + 1)
+    # fp16 biases (as Int8Linear's) need fp16 activations on the CPU oracle's F.linear
+    x = torch.randn(M, 1024, generator=g).to(torch.float16 if bias else torch.bfloat16)
+    print(f"  Int8SwiGLU M={M} bias={bias}", flush=True)
+    y = q.to(gpu)(x.to(gpu)).cpu()
+    qc = q.cpu()
+    ref = fallback.swiglu_ffn_ref(x, qc.weight_gate_up, qc.scale_gate_up, qc.weight_down, qc.scale_down,
+                                  qc.bias_gate_up, qc.bias_down)
+    assert y.dtype == ref.dtype and y.shape == ref.shape
+    torch.testing.assert_close(y.float(), ref.float(), rtol=1e-2, atol=1e-2)
+
+
 def test_rmsnorm_golden(gpu, golden):
     x = _t16(golden["rms_x_bf16"], torch.bfloat16)
     w = _t16(golden["rms_w_bf16"], torch.bfloat16)
