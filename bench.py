@@ -302,6 +302,25 @@ def run_mlp(args, dev):
     rec = {"us_per_call": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
     out[f"rmsnorm_residual M={M}"] = rec
     log(f"rmsnorm_residual M={M} H={H} bf16: {rec}")
+    del xs, rs
+    # Int8 KV-cache codec (QuantizedTensor, per channel): one bf16 K or V block
+    # [batch 8, heads 32, seq 4096, head_dim 128] (256 MiB), 2 blocks cycled;
+    # reads 2 B and writes 1 B per element plus a 2-byte scale per row.
+    from rotalabs_accel.speculative import QuantizedTensor
+    shape = (8, 32, 4096, 128)
+    kvs = [torch.randn(shape, device=dev, generator=g).to(torch.bfloat16) for _ in range(2)]
+
+    class _Codec:
+        def run(self, n):
+            for i in range(n):
+                QuantizedTensor(kvs[i % 2], bits=8)
+    ms, _ = time_graph(_Codec(), 12, 4, per_graph=4)
+    elems = shape[0] * shape[1] * shape[2] * shape[3]
+    gbs = (3 * elems + 2 * elems // shape[3]) / (ms * 1e-3) / 1e9
+    rec = {"us_per_call": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+    out["kv_codec int8 bf16 [8,32,4096,128]"] = rec
+    log(f"kv codec int8 per-channel bf16 {list(shape)}: {rec}")
+    del kvs
     return out
 
 

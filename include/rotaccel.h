@@ -157,6 +157,22 @@ int ra_quantize_per_channel(const void *w, int64_t ldw, int w_dtype,
                             int64_t N, int64_t K,
                             int8_t *q, int64_t ldq, float *scale, void *stream);
 
+/*
+ * Per-row symmetric quantisation of a tensor viewed as [rows, cols] (the
+ * last dimension is the row), as the KV-cache codec QuantizedTensor(t, bits,
+ * per_channel=True) computes it on the CPU
+ * (src/rotalabs_accel/speculative/kv_compression.py:51-78): with every
+ * intermediate rounded to t_dtype, s = max(amax / qmax, 1e-8) with
+ * qmax = 2^(bits-1) - 1, q = clamp(round_half_even(t / s), -qmax-1, qmax)
+ * (an all-zero fp16 row, whose floor rounds to 0, gives q = 0).
+ * q: int8 [rows, ldq]; scale: [rows] in t_dtype. bits: 8 or 4 (4-bit values
+ * are stored one per int8, as the reference does).
+ * No counterpart on the reference's GPU: it runs torch ops on any device.
+ */
+int ra_quantize_rows(const void *t, int64_t ldt, int t_dtype,
+                     int64_t rows, int64_t cols, int bits,
+                     int8_t *q, int64_t ldq, void *scale, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,18 @@ def rmsnorm_residual_ref(x: torch.Tensor, r: torch.Tensor, w: torch.Tensor, eps:
     return (v * rr).to(x.dtype) * w
 
 
+def quantized_tensor_ref(t: torch.Tensor, bits: int = 8, per_channel: bool = True):
+    """kv_compression.py:51-78 (QuantizedTensor.__init__) on a CPU tensor:
+    returns (data int8, scale)."""
+    qmax = 2 ** (bits - 1) - 1
+    if per_channel:
+        scale = (t.abs().amax(dim=-1, keepdim=True) / qmax).clamp(min=1e-8)
+    else:
+        scale = max((t.abs().max() / qmax).item(), 1e-8)
+    lo = -128 if bits == 8 else -8
+    return (t / scale).round().clamp(lo, qmax).to(torch.int8), scale
+
+
 def swiglu_ref(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """activations.py:36-45 on CPU tensors."""
     return F.silu(gate) * up

@@ -116,3 +116,25 @@ def calculate_quantization_error(orig32: np.ndarray, q: np.ndarray, scale: np.nd
         "relative_error_pct": rel,
         "snr_db": float(10 * np.log10(signal / (noise + 1e-10))),
     }
+
+
+# ------------------------------------------------------------ KV-cache codec
+def quantized_tensor_rows(t32: np.ndarray, dtype: str = "f32", bits: int = 8):
+    """Closed form of QuantizedTensor(t, bits, per_channel=True)
+    (src/rotalabs_accel/speculative/kv_compression.py:51-78) over the last
+    dimension, every step rounded to ``dtype`` as the CPU tensor ops do:
+      scale = round(|t|.amax(-1) / qmax), qmax = 2^(bits-1) - 1      (:64)
+      scale = round(max(scale, 1e-8))                               (:65)
+      q     = int8(clamp(rne(round(t / scale)), -qmax-1, qmax))     (:70-75)
+    NaN ratios (0/0 of an all-zero row whose floor underflows in fp16)
+    convert to 0. Returns (q int8, scale fp32 values of ``dtype``)."""
+    t32 = np.asarray(t32, dtype=np.float32)
+    qmax = (1 << (bits - 1)) - 1
+    a = np.abs(t32).max(axis=-1, keepdims=True) if t32.shape[-1] else np.zeros(t32.shape[:-1] + (1,), np.float32)
+    scale = round_to((a / np.float32(qmax)).astype(np.float32), dtype)
+    scale = round_to(np.maximum(scale, np.float32(1e-8)).astype(np.float32), dtype)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        ratio = round_to((t32 / scale).astype(np.float32), dtype)
+    r = np.rint(ratio)
+    q = np.where(np.isnan(r), 0, np.clip(r, -qmax - 1, qmax)).astype(np.int8)
+    return q, scale

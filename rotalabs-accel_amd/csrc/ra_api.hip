@@ -197,4 +197,15 @@ int ra_quantize_per_channel(const void *w, int64_t ldw, int w_dtype, int64_t N, 
   return to_status(quantize_launch(w, ldw, w_dtype, N, K, q, ldq, scale, static_cast<hipStream_t>(stream)));
 }
 
+int ra_quantize_rows(const void *t, int64_t ldt, int t_dtype, int64_t rows, int64_t cols, int bits, int8_t *q,
+                     int64_t ldq, void *scale, void *stream) {
+  if (rows < 0 || cols < 0 || rows > INT32_MAX || cols > INT32_MAX) return RA_ERR_ARG;
+  if (bits != 8 && bits != 4) return RA_ERR_ARG;
+  if (!valid_act(t_dtype)) return RA_ERR_DTYPE;
+  if (rows == 0 || cols == 0) return RA_OK;
+  if (!t || !q || !scale || ldt < cols || ldq < cols) return RA_ERR_ARG;
+  return to_status(quantize_rows_launch(t, ldt, t_dtype, rows, cols, bits, q, ldq, scale,
+                                        static_cast<hipStream_t>(stream)));
+}
+
 }  // extern "C"

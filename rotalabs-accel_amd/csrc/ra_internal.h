@@ -81,5 +81,7 @@ hipError_t rmsnorm_launch(const void *x, int64_t ldx, int x_dt, const void *r, i
 hipError_t swiglu_launch(const void *g, const void *u, void *o, int64_t n, int dt, hipStream_t s);
 hipError_t quantize_launch(const void *w, int64_t ldw, int w_dt, int64_t N, int64_t K, int8_t *q,
                            int64_t ldq, float *scale, hipStream_t s);
+hipError_t quantize_rows_launch(const void *t, int64_t ldt, int t_dt, int64_t rows, int64_t cols, int bits,
+                                int8_t *q, int64_t ldq, void *scale, hipStream_t s);
 
 }  // namespace ra

@@ -201,4 +201,37 @@ hipError_t quantize_launch(const void *w, int64_t ldw, int w_dt, int64_t N, int6
   return hipGetLastError();
 }
 
+// Per-row symmetric quantisation of a KV-cache tensor, as QuantizedTensor
+// (src/rotalabs_accel/speculative/kv_compression.py:51-78, per_channel) on
+// the CPU, with every intermediate in the tensor's dtype t:
+//   s = round_t(max(round_t(amax / qmax), 1e-8))      qmax = 2^(bits-1) - 1
+//   q = int8(clamp(rint(round_t(x / s)), -qmax-1, qmax)), NaN -> 0
+// (fp16 rounds the 1e-8 floor to 0, so an all-zero row gives 0/0 = NaN, which
+// the CPU's float -> int8 conversion turns into 0). The scale is stored in t.
+__global__ __launch_bounds__(kRowThreads) void quantize_rows_kernel(const void *__restrict__ t, int64_t ldt,
+                                                                    int t_dt, int cols, int qmax,
+                                                                    int8_t *__restrict__ q, int64_t ldq,
+                                                                    void *__restrict__ scale) {
+  __shared__ float smem[kRowThreads / 64];
+  const int64_t row = blockIdx.x;
+  float amax = 0.f;
+  for (int i = threadIdx.x; i < cols; i += kRowThreads)
+    amax = fmaxf(amax, fabsf(load_as_f32(t, row * ldt + i, t_dt)));
+  amax = block_reduce<true>(amax, smem);
+  const float s = round_through(fmaxf(round_through(amax / (float)qmax, t_dt), 1e-8f), t_dt);
+  for (int i = threadIdx.x; i < cols; i += kRowThreads) {
+    const float v = round_through(load_as_f32(t, row * ldt + i, t_dt) / s, t_dt);
+    const float r = rintf(v);
+    q[row * ldq + i] = r != r ? (int8_t)0 : (int8_t)(int)fminf(fmaxf(r, (float)(-qmax - 1)), (float)qmax);
+  }
+  if (threadIdx.x == 0) store_from_f32(scale, row, t_dt, s);
+}
+
+hipError_t quantize_rows_launch(const void *t, int64_t ldt, int t_dt, int64_t rows, int64_t cols, int bits,
+                                int8_t *q, int64_t ldq, void *scale, hipStream_t s) {
+  hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)rows), dim3(kRowThreads), 0, s, t, ldt, t_dt, (int)cols,
+                     (1 << (bits - 1)) - 1, q, ldq, scale);
+  return hipGetLastError();
+}
+
 }  // namespace ra

@@ -47,6 +47,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "ra_rmsnorm_residual": ([p, i64, i32, p, i64, i32, p, i32, p, i64, i32, i64, i64, f32, p], i32),
         "ra_swiglu": ([p, p, p, i64, i32, p], i32),
         "ra_quantize_per_channel": ([p, i64, i32, i64, i64, p, i64, p, p], i32),
+        "ra_quantize_rows": ([p, i64, i32, i64, i64, i32, p, i64, p, p], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

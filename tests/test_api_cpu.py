@@ -111,6 +111,56 @@ def test_swiglu_modules_cpu(bias):
         ra.Int8SwiGLU(64, 96)(xh)
 
 
+def test_quantized_tensor_codec_cpu():
+    """QuantizedTensor keeps the reference's attributes and runs its torch
+    ops on CPU tensors (per-channel and per-tensor, 8 and 4 bits)."""
+    from rotalabs_accel.speculative import QuantizedTensor
+    g = torch.Generator().manual_seed(17)
+    t = torch.randn(2, 4, 16, 64, generator=g).to(torch.bfloat16)
+    for bits in (8, 4):
+        for per_channel in (True, False):
+            qt = QuantizedTensor(t, bits=bits, per_channel=per_channel)
+            q, s = fallback.quantized_tensor_ref(t, bits, per_channel)
+            assert torch.equal(qt.data, q)
+            assert (torch.equal(qt.scale, s) if per_channel else qt.scale == s)
+            assert qt.shape == t.shape and qt.dtype == t.dtype and qt.bits == bits
+            assert torch.equal(qt.dequantize(), q.to(t.dtype) * s)
+            n = t.numel() * (1 if bits == 8 else 0.5) + (qt.scale.numel() * 4 if per_channel else 4)
+            assert qt.memory_bytes == int(n)
+    with pytest.raises(ValueError, match="Unsupported bits"):
+        QuantizedTensor(t, bits=2)
+
+
+@pytest.mark.parametrize("cls_name", ["QuantizedLinear", "Int8Linear"])
+def test_quantize_model(cls_name):
+    """quantize_model replaces every nn.Linear (skip list honoured), the
+    outputs follow the int8 modules, and the state_dict reloads."""
+    from rotalabs_accel.quantization import quantize_model
+    cls = getattr(ra, cls_name)
+    torch.manual_seed(5)
+    model = torch.nn.Sequential(torch.nn.Linear(64, 128), torch.nn.ReLU(),
+                                torch.nn.Sequential(torch.nn.Linear(128, 96, bias=False)),
+                                torch.nn.Linear(96, 32))
+    x = torch.randn(4, 64)
+    ref = model(x)
+    quantize_model(model, cls, skip=["3"])
+    assert isinstance(model[0], cls) and isinstance(model[2][0], cls)
+    assert type(model[3]) is torch.nn.Linear
+    xin = x.half() if cls_name == "Int8Linear" else x
+    if cls_name == "Int8Linear":   # fp16 activations and bias (as the reference module)
+        model[3] = model[3].half()
+    y = model(xin)
+    assert torch.allclose(y.float(), ref, rtol=5e-2, atol=5e-2)
+    sd = model.state_dict()
+    assert "0.weight_int8" in sd and "2.0.weight_int8" in sd
+    fresh = torch.nn.Sequential(cls(64, 128, bias=True), torch.nn.ReLU(),
+                                torch.nn.Sequential(cls(128, 96)), model[3])
+    fresh.load_state_dict(sd)
+    for m in (fresh[0], fresh[2][0]):
+        m._quantized = True
+    assert torch.equal(fresh(xin), y)
+
+
 def test_quantize_fp32_bit_exact():
     g = torch.Generator().manual_seed(11)
     w = torch.randn(96, 257, generator=g) * 0.02

@@ -145,6 +145,25 @@ def test_int8_swiglu_module_vs_oracle(gpu, M, bias):
     torch.testing.assert_close(y.float(), ref.float(), rtol=1e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bits", [8, 4])
+def test_kv_codec_rows_bit_exact(gpu, dt, bits):
+    """ra_quantize_rows (QuantizedTensor, per channel) on the GPU equals the
+    CPU arithmetic bit for bit: data and scale, all-zero rows included."""
+    from rotalabs_accel.speculative import QuantizedTensor
+    g = torch.Generator().manual_seed(bits + 3)
+    t = (torch.randn(3, 8, 37, 128, generator=g) * 4).to(dt)
+    t[0, 0, 0] = 0
+    t[1, 2, 5, :] = 2.5
+    print(f"  kv codec {dt} bits={bits}", flush=True)
+    qt = QuantizedTensor(t.to(gpu), bits=bits)
+    q, s = fallback.quantized_tensor_ref(t, bits)
+    assert qt.data.shape == t.shape and qt.scale.shape == t.shape[:-1] + (1,)
+    assert qt.scale.dtype == dt
+    assert torch.equal(qt.data.cpu(), q) and torch.equal(qt.scale.cpu(), s)
+    assert torch.equal(qt.dequantize().cpu(), q.to(dt) * s)
+
+
 def test_rmsnorm_golden(gpu, golden):
     x = _t16(golden["rms_x_bf16"], torch.bfloat16)
     w = _t16(golden["rms_w_bf16"], torch.bfloat16)

@@ -214,3 +214,31 @@ def test_rmsnorm_residual_oracle_pinned(golden):
     v = xh.double() + rf.double()
     n = (v / torch.sqrt((v * v).mean(dim=-1, keepdim=True) + 1e-6)).half().double() * wf.double()
     assert torch.allclose(y.double(), n, rtol=2 ** -10, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("bits", [8, 4])
+def test_kv_codec_restatements_agree(dtype, bits):
+    """The KV-cache codec (kv_compression.py:51-78) restated twice -- numpy
+    closed form with explicit roundings, and the reference's torch ops on the
+    CPU -- agree bit for bit, including all-zero rows (fp16's 1e-8 floor
+    underflows: 0/0 -> 0), exact .5 ties and rows of one repeated value; the
+    invariants |q| <= qmax and |q| = qmax at each row's |max| (fp32; >= qmax-1
+    when the scale is rounded to 16 bits) hold."""
+    g = torch.Generator().manual_seed(bits)
+    tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[dtype]
+    t = (torch.randn(6, 40, generator=g) * 3).to(tdt)
+    t[1] = 0
+    t[2, :] = 2.5                                   # one repeated value
+    qmax = 2 ** (bits - 1) - 1
+    t[3, 0] = float(qmax)                            # scale 1 (exactly representable)
+    t[3, 1:6] = torch.tensor([0.5, 1.5, 2.5, -0.5, -1.5])
+    qt, st = fallback.quantized_tensor_ref(t, bits)
+    qn, sn = oq.quantized_tensor_rows(t.float().numpy(), dtype, bits)
+    assert np.array_equal(qt.numpy(), qn)
+    assert np.array_equal(st.float().numpy(), sn)
+    assert qt[3, 1:6].tolist() == [0, 2, 2, 0, -2]  # round half to even
+    assert (qt.abs() <= qmax).all() and (qt[1] == 0).all()
+    nz = t.abs().amax(dim=-1) > 0
+    # the scale rounded to a 16-bit dtype can exceed amax / qmax by half an ulp
+    assert (qt.abs().amax(dim=-1)[nz] >= (qmax if dtype == "f32" else qmax - 1)).all()
