@@ -227,10 +227,91 @@ __global__ __launch_bounds__(kRowThreads) void quantize_rows_kernel(const void *
   if (threadIdx.x == 0) store_from_f32(scale, row, t_dt, s);
 }
 
+// Same arithmetic for short 16-bit rows (cols % 8 == 0, cols <= 512, 16-byte
+// aligned rows; e.g. head_dim-wide KV rows): L = cols / 8 lanes per row
+// (rounded up to a power of two), 64 / L rows per wave, each lane one 16-byte
+// chunk of 8 values (4 rows' chunks loaded at once), the row maximum by lane
+// shuffles within the group, 8-byte stores of the 8 quantised values -- no
+// per-row workgroup.
+template <int DT, int L>
+__global__ __launch_bounds__(256) void quantize_rows_short_kernel(const uint16_t *__restrict__ t, int64_t ldt,
+                                                                  int64_t rows, int cols, int qmax,
+                                                                  int8_t *__restrict__ q, int64_t ldq,
+                                                                  uint16_t *__restrict__ scale) {
+  using A = Act<DT>;
+  constexpr int U = 4;                       // rows per lane group, loads in flight together
+  constexpr int RPW = 64 / L;                // rows per wave and pass
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int c = lane % L;                    // 16-byte chunk of this lane
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wid) * (RPW * U) + lane / L;
+  const int cc = 8 * c < cols ? c : 0;       // clamped: loads stay unconditional
+  uint4 v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    int64_t rr = row0 + (int64_t)u * RPW;
+    rr = rr < rows ? rr : rows - 1;
+    v[u] = *reinterpret_cast<const uint4 *>(t + rr * ldt + 8 * cc);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t row = row0 + (int64_t)u * RPW;
+    const bool live = row < rows && 8 * c < cols;
+    const uint16_t *h = reinterpret_cast<const uint16_t *>(&v[u]);
+    float x[8], amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = A::in(h[e]);
+      amax = fmaxf(amax, fabsf(x[e]));
+    }
+    if (!live) amax = 0.f;
+#pragma unroll
+    for (int off = L / 2; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    const float sc = A::rnd(fmaxf(A::rnd(amax / (float)qmax), 1e-8f));
+    if (!live) continue;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float r = rintf(A::rnd(x[e] / sc));
+      const int qi = r != r ? 0 : (int)fminf(fmaxf(r, (float)(-qmax - 1)), (float)qmax);
+      const uint32_t b = (uint32_t)(uint8_t)(int8_t)qi;
+      if (e < 4) lo |= b << (8 * e);
+      else hi |= b << (8 * (e - 4));
+    }
+    store8(q + row * ldq + 8 * c, lo, hi);
+    if (c == 0) scale[row] = A::out(sc);
+  }
+}
+
+template <int DT>
+static void quantize_rows_short_launch(const void *t, int64_t ldt, int64_t rows, int cols, int qmax, int8_t *q,
+                                       int64_t ldq, void *scale, hipStream_t s) {
+  const uint16_t *tp = static_cast<const uint16_t *>(t);
+  uint16_t *sp = static_cast<uint16_t *>(scale);
+  const int need = cols / 8;
+#define RA_QROWS(L_)                                                                                \
+  if (need <= L_) {                                                                                 \
+    const int64_t blocks = (rows + 4 * 4 * (64 / L_) - 1) / (4 * 4 * (64 / L_));                  \
+    hipLaunchKernelGGL((quantize_rows_short_kernel<DT, L_>), dim3((unsigned)blocks), dim3(256), 0, s, tp, ldt, \
+                       rows, cols, qmax, q, ldq, sp);                                               \
+    return;                                                                                         \
+  }
+  RA_QROWS(1) RA_QROWS(2) RA_QROWS(4) RA_QROWS(8) RA_QROWS(16) RA_QROWS(32) RA_QROWS(64)
+#undef RA_QROWS
+}
+
 hipError_t quantize_rows_launch(const void *t, int64_t ldt, int t_dt, int64_t rows, int64_t cols, int bits,
                                 int8_t *q, int64_t ldq, void *scale, hipStream_t s) {
+  const int qmax = (1 << (bits - 1)) - 1;
+  const bool short_rows = (t_dt == RA_F16 || t_dt == RA_BF16) && cols % 8 == 0 && cols <= 512 && ldt % 8 == 0 &&
+                          ldq % 8 == 0 && !(reinterpret_cast<uintptr_t>(t) & 15) &&
+                          !(reinterpret_cast<uintptr_t>(q) & 7) && rows * 64 < ((int64_t)1 << 31);
+  if (short_rows) {
+    if (t_dt == RA_F16) quantize_rows_short_launch<RA_F16>(t, ldt, rows, (int)cols, qmax, q, ldq, scale, s);
+    else quantize_rows_short_launch<RA_BF16>(t, ldt, rows, (int)cols, qmax, q, ldq, scale, s);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)rows), dim3(kRowThreads), 0, s, t, ldt, t_dt, (int)cols,
-                     (1 << (bits - 1)) - 1, q, ldq, scale);
+                     qmax, q, ldq, scale);
   return hipGetLastError();
 }
 

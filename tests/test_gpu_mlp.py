@@ -147,12 +147,14 @@ def test_int8_swiglu_module_vs_oracle(gpu, M, bias):
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("bits", [8, 4])
-def test_kv_codec_rows_bit_exact(gpu, dt, bits):
+@pytest.mark.parametrize("cols", [128, 200, 36, 1000])
+def test_kv_codec_rows_bit_exact(gpu, dt, bits, cols):
     """ra_quantize_rows (QuantizedTensor, per channel) on the GPU equals the
-    CPU arithmetic bit for bit: data and scale, all-zero rows included."""
+    CPU arithmetic bit for bit: data and scale, all-zero rows included (short
+    rows: several per wave; others: a workgroup per row)."""
     from rotalabs_accel.speculative import QuantizedTensor
     g = torch.Generator().manual_seed(bits + 3)
-    t = (torch.randn(3, 8, 37, 128, generator=g) * 4).to(dt)
+    t = (torch.randn(3, 8, 37, cols, generator=g) * 4).to(dt)
     t[0, 0, 0] = 0
     t[1, 2, 5, :] = 2.5
     print(f"  kv codec {dt} bits={bits}", flush=True)
