@@ -13,6 +13,9 @@ Metric: int8_gemm HBM GB/s at M=1 and TFLOP/s at M=2048 (K=4096, N=11008).
 * ``roofline``: the dominant kernel's achieved GB/s (TFLOP/s for prefill)
   from HIP events on the launch stream, against MI355X peaks (HBM 8 TB/s,
   dense fp16 MFMA 2516.6 TFLOP/s).
+* ``w8a8``: the opt-in W8A8 route (int8 activations, int8 MFMA) at the
+  prefill shape, TOPS against the dense int8 peak (5033 TOP/s), beside
+  hipBLASLt's int8 GEMM (torch._int_mm).
 * ``mlp``: the fused decoder MLP block (RMSNorm -> int8 gate/up + SwiGLU ->
   int8 down, bf16, H=8192, I=28672) per call at M=1 (GB/s) and M=4096
   (TFLOP/s), graph replay.
@@ -53,7 +56,7 @@ def parse():
     p.add_argument("--prefill-steps", type=int, default=300)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", choices=("all", "decode", "prefill", "mlp"), default="all",
+    p.add_argument("--only", choices=("all", "decode", "prefill", "mlp", "w8a8"), default="all",
                    help="run one workload only (for profiler runs)")
     p.add_argument("--no-mlp", action="store_true", help="skip the fused-MLP timing")
     p.add_argument("--no-graph", action="store_true",
@@ -251,6 +254,72 @@ def run_prefill(args, dev):
     return pms, tflops, pvariant
 
 
+PEAK_INT8_TOPS = 5033.2   # dense int8 MFMA (v_mfma_i32_32x32x32_i8)
+
+
+def run_w8a8(args, dev):
+    """Opt-in W8A8 route at the prefill shape (M=2048, K=4096, N=11008, fp16):
+    activation quantisation + int8 MFMA GEMM, pre-bound C ABI calls replayed
+    in a HIP graph; the GEMM alone; hipBLASLt's int8 GEMM (torch._int_mm) at
+    the same shape for comparison. Returns a dict for the JSON line."""
+    import torch
+    from rotalabs_accel import _backend
+    from rotalabs_accel.kernels import quantized_matmul as qm
+    from workloads import gemm_case, gemm_flops
+    Mp, Kp, Np, seedp = PREFILL
+    cp = gemm_case(Mp, Kp, Np, seedp, device=dev)
+    lib = _backend.load()
+    xq = torch.empty((Mp, Kp), dtype=torch.int8, device=dev)
+    xs = torch.empty((Mp,), dtype=torch.float16, device=dev)
+    y = torch.empty((Mp, Np), dtype=torch.float16, device=dev)
+    wcopies = [cp.q, cp.q.clone(), cp.q.clone()]
+    ref = qm.int8_gemm(cp.x, cp.q, cp.s, use_cublas=True)
+
+    class _Route:
+        def __init__(self, quant=True):
+            self.quant = quant
+
+        def run(self, n):
+            st = torch.cuda.current_stream().cuda_stream
+            for i in range(n):
+                if self.quant:
+                    _backend.check(lib.ra_quantize_act_rows(cp.x.data_ptr(), Kp, _backend.F16, Mp, Kp,
+                                                            xq.data_ptr(), Kp, xs.data_ptr(), st))
+                _backend.check(lib.ra_w8a8_gemm(xq.data_ptr(), Kp, xs.data_ptr(), wcopies[i % 3].data_ptr(), Kp,
+                                                cp.s.data_ptr(), None, 0, y.data_ptr(), Np, _backend.F16,
+                                                Mp, Np, Kp, st))
+    _Route().run(1)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref), "timed W8A8 path differs from int8_gemm(use_cublas=True)"
+    steps = max(30, args.prefill_steps // 2)
+    route_ms, _ = time_graph(_Route(True), steps, 3, per_graph=9)
+    gemm_ms, _ = time_graph(_Route(False), steps, 3, per_graph=9)
+
+    class _IntMM:
+        def run(self, n):
+            for i in range(n):
+                torch._int_mm(xq, wcopies[i % 3].t())
+    try:
+        imm_ms, _ = time_graph(_IntMM(), steps, 3, per_graph=9)
+    except RuntimeError as e:          # hipBLASLt refusing the shape is not fatal here
+        log(f"torch._int_mm comparison skipped: {e}")
+        imm_ms = float("nan")
+    ops = gemm_flops(Mp, Kp, Np)
+    tops = ops / (gemm_ms * 1e-3) / 1e12
+    rec = {
+        "workload": f"W8A8 route M={Mp} K={Kp} N={Np} fp16 (opt-in: int8_gemm(..., use_cublas=True))",
+        "route_us": round(route_ms * 1e3, 2),
+        "route_TOPS": round(ops / (route_ms * 1e-3) / 1e12, 1),
+        "gemm_us": round(gemm_ms * 1e3, 2),
+        "gemm_TOPS": round(tops, 1),
+        "frac_int8_peak": round(tops / PEAK_INT8_TOPS, 4),
+        "hipblaslt_int_mm_us": round(imm_ms * 1e3, 2),
+        "hipblaslt_int_mm_TOPS": round(ops / (imm_ms * 1e-3) / 1e12, 1),
+    }
+    log(f"w8a8: {rec}")
+    return rec
+
+
 MLP = (8192, 28672)   # hidden, intermediate (70B-class decoder MLP, bf16)
 
 
@@ -362,6 +431,9 @@ def main():
     pvariant = None
     if args.only in ("all", "prefill"):
         pms, tflops, pvariant = run_prefill(args, dev)
+    w8a8 = None
+    if args.only in ("all", "w8a8"):
+        w8a8 = run_w8a8(args, dev)
     mlp = None
     if args.only == "mlp" or (args.only == "all" and not args.no_mlp):
         mlp = run_mlp(args, dev)
@@ -413,6 +485,8 @@ def main():
                                                      VARIANT_KERNELS.get(pvariant, ""))},
         },
     }
+    if w8a8 is not None:
+        out["w8a8"] = w8a8
     if mlp is not None:
         out["mlp"] = {"workload": "fused decoder MLP (RMSNorm -> int8 gate/up + SwiGLU -> int8 down), bf16, "
                                   "H=8192, I=28672, random int8 per-channel weights", **mlp}

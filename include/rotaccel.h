@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define RA_ABI_VERSION 2
+#define RA_ABI_VERSION 3
 
 enum ra_dtype { RA_F16 = 0, RA_BF16 = 1, RA_F32 = 2 };
 
@@ -172,6 +172,39 @@ int ra_quantize_per_channel(const void *w, int64_t ldw, int w_dtype,
 int ra_quantize_rows(const void *t, int64_t ldt, int t_dtype,
                      int64_t rows, int64_t cols, int bits,
                      int8_t *q, int64_t ldq, void *scale, void *stream);
+
+/*
+ * W8A8 route, step 1: per-row dynamic int8 quantisation of the activations
+ * x[M,K] (fp16 or bf16), as _int8_gemm_cublas computes it
+ * (src/rotalabs_accel/kernels/quantized_matmul.py:85-87), every op rounded to
+ * x_dtype as torch does: a = max(max_k |x[m,k]|, 1e-5) (NaN propagates),
+ * xs[m] = a / 127, mult = reciprocal(a) * 127 (torch's evaluation of 127 / a),
+ * q[m,k] = clamp(round_half_even(x[m,k] * mult), -128, 127) (NaN -> 0).
+ * q: int8 [M, ldq]; xs: [M] in x_dtype. K = 0 is an error (as torch's
+ * amax over an empty row is).
+ */
+int ra_quantize_act_rows(const void *x, int64_t ldx, int x_dtype,
+                         int64_t M, int64_t K,
+                         int8_t *q, int64_t ldq, void *xs, void *stream);
+
+/*
+ * W8A8 route, step 2: int8 x int8 GEMM on the int8 matrix cores,
+ *   y[m,n] = (float(sum_k xq[m,k] * w[n,k]) * xs[m]) * scale[n] (+ bias[n])
+ * with exact int32 sums and fp32 scaling rounded once to y_dtype. Replaces
+ * torch._int_mm (quantized_matmul.py:93) and _dequantize_output (:38-40,
+ * :99-100), which converts the int32 sums to fp16 first (|sum| > 65504
+ * becomes inf there); the fp32 scaling is that of the reference's fused
+ * int8 kernel (:259). bias (added as in :474-476) is optional.
+ * xq: int8 [M, ldxq]; xs: [M] in y_dtype (fp16 or bf16, the activation
+ * dtype); w: int8 [N, ldw]; scale: fp32 [N]; y: [M, ldy] in y_dtype.
+ * K % 128 == 0 with 16-byte aligned rows runs the MFMA kernel, anything else
+ * a slow VALU kernel.
+ */
+int ra_w8a8_gemm(const int8_t *xq, int64_t ldxq, const void *xs,
+                 const int8_t *w, int64_t ldw, const float *scale,
+                 const void *bias, int bias_dtype,
+                 void *y, int64_t ldy, int y_dtype,
+                 int64_t M, int64_t N, int64_t K, void *stream);
 
 #ifdef __cplusplus
 }

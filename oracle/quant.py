@@ -138,3 +138,40 @@ def quantized_tensor_rows(t32: np.ndarray, dtype: str = "f32", bits: int = 8):
     r = np.rint(ratio)
     q = np.where(np.isnan(r), 0, np.clip(r, -qmax - 1, qmax)).astype(np.int8)
     return q, scale
+
+
+# ------------------------------------------------------------- W8A8 route
+def quantize_activations_rows(x32: np.ndarray, dtype: str = "f16"):
+    """Closed form of the activation quantisation of _int8_gemm_cublas
+    (src/rotalabs_accel/kernels/quantized_matmul.py:85-87) over rows of
+    x (M, K), every op rounded to ``dtype`` as torch's tensor ops do:
+      a    = max(|x|.amax(1), round(1e-5))          (:85; NaN propagates)
+      xs   = round(a / 127)                         (:86)
+      mult = round(round(1 / a) * 127)              (:87; torch evaluates
+                                                     127 / a as reciprocal * 127)
+      q    = int8(clamp(rne(round(x * mult)), -128, 127)), NaN -> 0
+    Returns (q int8 (M, K), xs fp32 values of ``dtype`` (M,))."""
+    x32 = np.asarray(x32, dtype=np.float32)
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        a = np.abs(x32).max(axis=1)
+        a = np.maximum(a, round_to(np.float32(1e-5).reshape(1), dtype)[0]).astype(np.float32)
+        xs = round_to((a / np.float32(127)).astype(np.float32), dtype)
+        recip = round_to((np.float32(1) / a).astype(np.float32), dtype)
+        mult = round_to((recip * np.float32(127)).astype(np.float32), dtype)
+        r = np.rint(round_to((x32 * mult[:, None]).astype(np.float32), dtype))
+    q = np.where(np.isnan(r), 0, np.clip(r, -128, 127)).astype(np.int8)
+    return q, xs
+
+
+def w8a8_gemm_rows(xq: np.ndarray, xs32: np.ndarray, q: np.ndarray, s32: np.ndarray,
+                   dtype: str = "f16", bias32: np.ndarray | None = None) -> np.ndarray:
+    """The W8A8 GEMM as the reference's fused int8 kernel scales it
+    (quantized_matmul.py:259): exact integer sums, then in fp32 with each op
+    rounded, (float(sum) * xs[m]) * s[n] (+ bias[n]), rounded once to
+    ``dtype``. Returns fp32 values of ``dtype`` (M, N)."""
+    acc = xq.astype(np.int64) @ q.astype(np.int64).T
+    y = (acc.astype(np.float32) * np.asarray(xs32, np.float32)[:, None]).astype(np.float32)
+    y = (y * np.asarray(s32, np.float32)[None, :]).astype(np.float32)
+    if bias32 is not None:
+        y = (y + np.asarray(bias32, np.float32)[None, :]).astype(np.float32)
+    return round_to(y, dtype)

@@ -23,6 +23,7 @@ int g_tiled_mode = 0;
 int g_rows_rw = 0;
 int g_rows_pipe = 0;
 int g_batch_rt = 0;
+int g_w8a8_mode = 0;
 }
 #endif
 
@@ -75,6 +76,7 @@ void ra_tune_tiled(int mode) { ra::g_tiled_mode = mode; }
 void ra_tune_rows(int rw) { ra::g_rows_rw = rw; }
 void ra_tune_rows_pipe(int rp) { ra::g_rows_pipe = rp; }
 void ra_tune_batch_rt(int rt) { ra::g_batch_rt = rt; }
+void ra_tune_w8a8(int mode) { ra::g_w8a8_mode = mode; }
 #endif
 
 int ra_abi_version(void) { return RA_ABI_VERSION; }
@@ -206,6 +208,28 @@ int ra_quantize_rows(const void *t, int64_t ldt, int t_dtype, int64_t rows, int6
   if (!t || !q || !scale || ldt < cols || ldq < cols) return RA_ERR_ARG;
   return to_status(quantize_rows_launch(t, ldt, t_dtype, rows, cols, bits, q, ldq, scale,
                                         static_cast<hipStream_t>(stream)));
+}
+
+int ra_quantize_act_rows(const void *x, int64_t ldx, int x_dtype, int64_t M, int64_t K, int8_t *q, int64_t ldq,
+                         void *xs, void *stream) {
+  if (M < 0 || K < 0 || M > INT32_MAX || K > INT32_MAX) return RA_ERR_ARG;
+  if (x_dtype != RA_F16 && x_dtype != RA_BF16) return RA_ERR_DTYPE;
+  if (M == 0) return RA_OK;
+  if (K == 0 || !x || !q || !xs || ldx < K || ldq < K) return RA_ERR_ARG;  // torch's amax rejects K = 0
+  return to_status(quantize_act_launch(x, ldx, x_dtype, M, K, q, ldq, xs, static_cast<hipStream_t>(stream)));
+}
+
+int ra_w8a8_gemm(const int8_t *xq, int64_t ldxq, const void *xs, const int8_t *w, int64_t ldw, const float *scale,
+                 const void *bias, int bias_dtype, void *y, int64_t ldy, int y_dtype, int64_t M, int64_t N,
+                 int64_t K, void *stream) {
+  const W8A8Args a{xq, ldxq, xs, w, ldw, scale, bias, bias_dtype, y, ldy, y_dtype, M, N, K};
+  if (M < 0 || N < 0 || K < 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return RA_ERR_ARG;
+  if (y_dtype != RA_F16 && y_dtype != RA_BF16) return RA_ERR_DTYPE;
+  if (bias && !valid_act(bias_dtype)) return RA_ERR_DTYPE;
+  if (M == 0 || N == 0) return RA_OK;
+  if (!y || !xs || !scale || !w || (K > 0 && !xq)) return RA_ERR_ARG;
+  if (ldxq < K || ldw < K || ldy < N) return RA_ERR_ARG;
+  return to_status(w8a8_launch(a, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

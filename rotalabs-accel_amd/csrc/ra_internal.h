@@ -84,4 +84,24 @@ hipError_t quantize_launch(const void *w, int64_t ldw, int w_dt, int64_t N, int6
 hipError_t quantize_rows_launch(const void *t, int64_t ldt, int t_dt, int64_t rows, int64_t cols, int bits,
                                 int8_t *q, int64_t ldq, void *scale, hipStream_t s);
 
+// W8A8 (int8 activations x int8 weights on the int8 matrix cores).
+struct W8A8Args {
+  const int8_t *xq;  // [M, K] quantised activations, row stride ldxq
+  int64_t ldxq;
+  const void *xs;  // [M] activation scales, dtype y_dt
+  const int8_t *w;
+  int64_t ldw;
+  const float *scale;
+  const void *bias;  // may be null
+  int bias_dt;
+  void *y;
+  int64_t ldy;
+  int y_dt;
+  int64_t M, N, K;
+};
+hipError_t quantize_act_launch(const void *x, int64_t ldx, int x_dt, int64_t M, int64_t K, int8_t *q, int64_t ldq,
+                               void *xs, hipStream_t s);
+bool w8a8_tiled_supported(const W8A8Args &a);
+hipError_t w8a8_launch(const W8A8Args &a, hipStream_t s);
+
 }  // namespace ra

@@ -303,3 +303,31 @@ def test_missing_library_fails_loudly(tmp_path):
     env = dict(os.environ, ROTACCEL_LIB=str(tmp_path / "nope.so"))
     out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=300)
     assert "RAISED" in out.stdout and "Build it" in out.stdout
+
+
+@pytest.mark.parametrize("tdt,dt", [(torch.float16, "f16"), (torch.bfloat16, "bf16")])
+def test_w8a8_route_cpu_matches_oracle(tdt, dt):
+    """quantized_matmul.int8_gemm(use_cublas=True) on CPU tensors: activation
+    quantisation and the scaled int8 GEMM equal the numpy restatement bit for
+    bit; M <= 16 and use_cublas=None take the W8A16 route (reference dispatch
+    quantized_matmul.py:436-447)."""
+    from rotalabs_accel.kernels import quantized_matmul as qm
+    g = torch.Generator().manual_seed(11)
+    M, K, N = 40, 256, 96
+    x = torch.randn(2, M // 2, K, generator=g).to(tdt)
+    q, s = ra.quantize_weight_per_channel(torch.randn(N, K, generator=g))
+    b = torch.randn(N, generator=g).to(tdt)   # the CPU fallback's F.linear needs bias in x's dtype
+    y = qm.int8_gemm(x, q, s, b, use_cublas=True)
+    assert y.shape == (2, M // 2, N) and y.dtype == tdt
+    xq, xs = oq.quantize_activations_rows(x.reshape(-1, K).float().numpy(), dt)
+    ref = oq.w8a8_gemm_rows(xq, xs, q.numpy(), s.numpy(), dt, b.float().numpy())
+    np.testing.assert_array_equal(y.reshape(-1, N).float().numpy(), ref)
+    # the W8A8 error stays near the W8A16 result (activation quantisation)
+    y16 = qm.int8_gemm(x, q, s, b)
+    torch.testing.assert_close(y16, ra.int8_gemm(x, q, s, b), rtol=0, atol=0)
+    rel = (y.float() - y16.float()).norm() / y16.float().norm()
+    assert rel < 0.05
+    small = qm.int8_gemm(x[:, :8], q, s, b, use_cublas=True)
+    torch.testing.assert_close(small, ra.int8_gemm(x[:, :8], q, s, b), rtol=0, atol=0)
+    with pytest.raises(ValueError):
+        qm.quantize_activations(x, act_scale=100.0)

@@ -242,3 +242,84 @@ def test_kv_codec_restatements_agree(dtype, bits):
     nz = t.abs().amax(dim=-1) > 0
     # the scale rounded to a 16-bit dtype can exceed amax / qmax by half an ulp
     assert (qt.abs().amax(dim=-1)[nz] >= (qmax if dtype == "f32" else qmax - 1)).all()
+
+
+# ------------------------------------------------------------- W8A8 route
+def _act_rows(tdt, seed=0, M=48, K=300):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(M, K, generator=g) * torch.rand(M, 1, generator=g) * 8).to(tdt)
+    x[0] = 0                       # all-zero row: a = round(1e-5)
+    x[1, 3] = float("nan")         # NaN propagates through amax: q = 0, xs = NaN
+    x[2, 7] = float("inf")         # inf row: xs = inf, q = 0
+    x[3] = 1e-7                    # below the 1e-5 floor
+    x[4] = 3e-5
+    x[5] = -2.0                    # constant row: q = -127
+    x[6, :4] = torch.tensor([1.0, -1.0, 0.5, -0.5])  # tie candidates
+    x[7] = 60000.0 if tdt == torch.float16 else 3e38
+    return x
+
+
+@pytest.mark.parametrize("tdt,dt", [(torch.float16, "f16"), (torch.bfloat16, "bf16")])
+def test_w8a8_activation_quant_oracle_pinned(tdt, dt):
+    """The numpy restatement of quantized_matmul.py:85-87 equals torch's CPU
+    evaluation of the reference's own expression (which pins the rounding
+    model: 127 / a is reciprocal(a) * 127, each op rounded to the dtype; a
+    plain fp32 127 / a differs on a large share of rows), on random rows and
+    edge rows."""
+    x = _act_rows(tdt)
+    absmax = x.abs().amax(dim=1, keepdim=True).clamp(min=1e-5)
+    xs_t = (absmax / 127.0).to(tdt).reshape(-1)
+    q_t = (x * (127.0 / absmax)).round().clamp(-128, 127).to(torch.int8)
+    q, xs = oq.quantize_activations_rows(x.float().numpy(), dt)
+    np.testing.assert_array_equal(q, q_t.numpy())
+    np.testing.assert_array_equal(xs, xs_t.float().numpy())
+    # invariants: |q| <= 127 and the row max lands on +-127 (or 126 for a
+    # rounded multiplier) for every finite row above the floor
+    fin = np.isfinite(x.float().numpy()).all(1) & (np.abs(x.float().numpy()).max(1) > 1e-4)
+    assert np.abs(q.astype(int)).max() <= 128
+    assert (np.abs(q[fin].astype(int)).max(1) >= 126).all()
+    assert (q[1] == 0).all() and np.isnan(xs[1]) and np.isinf(xs[2]) and (q[2] == 0).all()
+    assert (q[5] == -127).all()
+
+
+def test_w8a8_scalar_division_forms_agree():
+    """a / 127 on the CPU (true division) and on CUDA (multiply by the fp32
+    reciprocal of a CPU scalar) round to the same 16-bit value for every
+    finite fp16 and bf16 a, so the restatement holds for either device."""
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    a16 = bits.view(np.float16).astype(np.float32)
+    a16 = a16[np.isfinite(a16)]
+    np.testing.assert_array_equal((a16 / np.float32(127)).astype(np.float16),
+                                  (a16 * (np.float32(1) / np.float32(127))).astype(np.float16))
+    ab = oq.bf16_bits_to_f32(bits)
+    ab = ab[np.isfinite(ab)]
+    np.testing.assert_array_equal(oq.round_to((ab / np.float32(127)).astype(np.float32), "bf16"),
+                                  oq.round_to((ab * (np.float32(1) / np.float32(127))).astype(np.float32), "bf16"))
+
+
+def test_w8a8_gemm_oracle_pinned():
+    """Integer sums against a brute-force triple loop; scaling against the
+    reference's fp16 dequantisation chain (quantized_matmul.py:38-40, run by
+    torch on the CPU) where that chain does not overflow (|sum| <= 65504),
+    and inf from that chain where it does."""
+    g = np.random.default_rng(3)
+    M, N, K = 5, 7, 64
+    xq = g.integers(-128, 128, (M, K)).astype(np.int8)
+    q = g.integers(-127, 128, (N, K)).astype(np.int8)
+    xs = oq.round_to(g.uniform(1e-3, 1e-1, M).astype(np.float32), "f16")
+    s = g.uniform(1e-4, 1e-2, N).astype(np.float32)
+    acc = np.array([[sum(int(xq[m, k]) * int(q[n, k]) for k in range(K)) for n in range(N)] for m in range(M)])
+    y = oq.w8a8_gemm_rows(xq, xs, q, s, "f16")
+    ref_chain = (torch.from_numpy(acc).to(torch.int32).half() * torch.from_numpy(xs).half()[:, None]
+                 * torch.from_numpy(s).half()[None, :]).float().numpy()
+    small = np.abs(acc) <= 65504
+    assert small.any() and (~small).any()
+    np.testing.assert_allclose(y[small], ref_chain[small], rtol=1e-2, atol=1e-2)
+    assert np.isinf(ref_chain[~small]).all() and np.isfinite(y).all()
+    # closed form: power-of-two scales keep the scaling exact
+    y2 = oq.w8a8_gemm_rows(xq, np.full(M, 2.0 ** -10, np.float32), q, np.full(N, 2.0 ** -6, np.float32), "f32")
+    np.testing.assert_array_equal(y2, acc.astype(np.float32) * 2.0 ** -16)
+    # bias is added after the scaling, in fp32
+    b = oq.round_to(g.uniform(-1, 1, N).astype(np.float32), "bf16")
+    y3 = oq.w8a8_gemm_rows(xq, xs, q, s, "f32", b)
+    np.testing.assert_array_equal(y3, oq.w8a8_gemm_rows(xq, xs, q, s, "f32") + b[None, :])
