@@ -197,8 +197,8 @@ int ra_quantize_act_rows(const void *x, int64_t ldx, int x_dtype,
  * int8 kernel (:259). bias (added as in :474-476) is optional.
  * xq: int8 [M, ldxq]; xs: [M] in y_dtype (fp16 or bf16, the activation
  * dtype); w: int8 [N, ldw]; scale: fp32 [N]; y: [M, ldy] in y_dtype.
- * K % 128 == 0 with 16-byte aligned rows runs the MFMA kernel, anything else
- * a slow VALU kernel.
+ * K % 64 == 0 with 16-byte aligned rows and row strides runs the MFMA
+ * kernel, anything else a slow VALU kernel.
  */
 int ra_w8a8_gemm(const int8_t *xq, int64_t ldxq, const void *xs,
                  const int8_t *w, int64_t ldw, const float *scale,

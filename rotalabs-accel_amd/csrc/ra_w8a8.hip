@@ -32,7 +32,7 @@
 namespace ra {
 
 #ifdef RA_TUNING
-extern int g_w8a8_mode;  // 0 auto; 1..3 force shape (4,4) (4,3) (4,2) with 64-k tiles; 11..13 with 128-k tiles
+extern int g_w8a8_mode;  // 0 auto; i forces configuration kCfgs[i - 1]
 #endif
 
 namespace w8a8 {
@@ -81,6 +81,58 @@ __global__ __launch_bounds__(kRowThreads) void quantize_act_kernel(const uint16_
   if (threadIdx.x == 0) xs[row] = A::out(A::rnd(a / 127.0f));
 }
 
+// The same for rows of K % 8 == 0, K <= 2048 * NC elements, 16-byte aligned:
+// each thread keeps NC chunks of 8 elements in registers (one 16-byte load
+// each), so the row is read once; 8-byte stores of the int8 values.
+template <int DT, int NC>
+__global__ __launch_bounds__(kRowThreads) void quantize_act_vec_kernel(const uint16_t *__restrict__ x, int64_t ldx,
+                                                                       int K, int8_t *__restrict__ q, int64_t ldq,
+                                                                       uint16_t *__restrict__ xs) {
+  using A = Act<DT>;
+  __shared__ float smem[2][kRowThreads / 64];
+  const int64_t row = blockIdx.x;
+  const uint4 *xr = reinterpret_cast<const uint4 *>(x + row * ldx);
+  const int chunks = K >> 3;
+  uint4 v[NC];
+  float amax = 0.f, nan = 0.f;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = threadIdx.x + j * kRowThreads;
+    v[j] = c < chunks ? xr[c] : uint4{0, 0, 0, 0};
+    const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+      const float f = A::in((uint16_t)(w[h >> 1] >> (16 * (h & 1))));
+      amax = fmaxf(amax, fabsf(f));
+      nan = f != f ? 1.f : nan;
+    }
+  }
+  amax = wave_max(amax);
+  nan = wave_max(nan);
+  if ((threadIdx.x & 63) == 0) smem[0][threadIdx.x >> 6] = amax, smem[1][threadIdx.x >> 6] = nan;
+  __syncthreads();
+  amax = fmaxf(fmaxf(smem[0][0], smem[0][1]), fmaxf(smem[0][2], smem[0][3]));
+  nan = fmaxf(fmaxf(smem[1][0], smem[1][1]), fmaxf(smem[1][2], smem[1][3]));
+  const float a = nan != 0.f ? __builtin_nanf("") : fmaxf(amax, A::rnd(1e-5f));
+  const float mult = A::rnd(A::rnd(1.0f / a) * 127.0f);
+  int8_t *qr = q + row * ldq;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = threadIdx.x + j * kRowThreads;
+    if (c >= chunks) break;
+    const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+    uint32_t packed[2] = {0, 0};
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+      const float r = rintf(A::rnd(A::in((uint16_t)(w[h >> 1] >> (16 * (h & 1)))) * mult));
+      const int qi = r != r ? 0 : (int)fminf(fmaxf(r, -128.0f), 127.0f);
+      packed[h >> 2] |= (uint32_t)(qi & 0xFF) << (8 * (h & 3));
+    }
+    store8(qr + 8 * c, packed[0], packed[1]);
+  }
+  if (threadIdx.x == 0) xs[row] = A::out(A::rnd(a / 127.0f));
+}
+
 // One output per thread, exact int32 sums; any K and layout.
 template <int DT>
 __global__ __launch_bounds__(256) void w8a8_generic_kernel(const int8_t *__restrict__ xq, int64_t ldxq,
@@ -107,7 +159,7 @@ __global__ __launch_bounds__(256) void w8a8_generic_kernel(const int8_t *__restr
 // share a bank window, so chunk c of row r sits at position c ^ ((r / P) % CPR):
 // the 16 lanes a ds_read_b128 serves per cycle (16 consecutive rows, one
 // chunk each) then hit 64 distinct banks.
-template <int BMB, int BNB, int BK_>
+template <int BMB, int BNB, int BK_, int OCC_>
 struct Tile {
   static constexpr int WM = 32 * BMB, WN = 32 * BNB;  // per-wave sub-tile
   static constexpr int BM = 2 * WM, BN = 2 * WN, BK = BK_;
@@ -117,7 +169,8 @@ struct Tile {
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int A_COPIES = A_BYTES / 4096, B_COPIES = B_BYTES / 4096;  // 1 KB copies per wave
   static constexpr int COPIES = A_COPIES + B_COPIES;
-  static constexpr int S = (160 * 1024) / STAGE < 6 ? (160 * 1024) / STAGE : 6;
+  static constexpr int OCC = OCC_;  // workgroups per CU (they share the 160 KB of LDS)
+  static constexpr int S = (160 * 1024 / OCC) / STAGE < 6 ? (160 * 1024 / OCC) / STAGE : 6;
   static_assert(BK == 64 || BK == 128, "K tile");
   static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "copies must split evenly over 4 waves");
   static_assert(S >= 2 && (S - 1) * COPIES <= 63, "pipeline depth");
@@ -220,15 +273,15 @@ __device__ __forceinline__ void epilogue(const i32x16 (&acc)[BMB][BNB], const ui
   }
 }
 
-template <int DT, int BMB, int BNB, int BK_>
-__global__ __launch_bounds__(256, 1) void w8a8_gemm_kernel(const int8_t *__restrict__ xq, int64_t ldxq,
+template <int DT, int BMB, int BNB, int BK_, int OCC_>
+__global__ __launch_bounds__(256, OCC_) void w8a8_gemm_kernel(const int8_t *__restrict__ xq, int64_t ldxq,
                                                            const uint16_t *__restrict__ xs,
                                                            const int8_t *__restrict__ w, int64_t ldw,
                                                            const float *__restrict__ scale,
                                                            const void *__restrict__ bias, int bias_dt,
                                                            uint16_t *__restrict__ y, int64_t ldy, int M, int N,
                                                            int K, int tiles_m, int tiles_n) {
-  using G = Tile<BMB, BNB, BK_>;
+  using G = Tile<BMB, BNB, BK_, OCC_>;
   constexpr int BM = G::BM, BN = G::BN, BK = G::BK, WM = G::WM, WN = G::WN, S = G::S;
   constexpr int CPR = G::CPR, RPC = G::RPC, P = G::P, NSUB = G::NSUB;
   constexpr int A_COPIES = G::A_COPIES, B_COPIES = G::B_COPIES, COPIES = G::COPIES;
@@ -408,15 +461,23 @@ __global__ __launch_bounds__(256, 1) void w8a8_gemm_kernel(const int8_t *__restr
   epilogue<DT, BMB, BNB>(acc, xs, scale, bias, bias_dt, y, ldy, M, N, m0 + wm * WM, g, n0 + wn * WN, l32);
 }
 
-struct Shape {
-  int bmb, bnb;
-  double cost;  // relative time per output at full occupancy
+// Tile configurations: 2 x 2 waves of (32 BMB) x (32 BNB) outputs, BK-k
+// stages, OCC workgroups per CU. `cost` is the relative time per output
+// when every CU is busy (measured at prefill shapes, M = 512..8192). Two
+// workgroups per CU (to overlap one's epilogue with the other's loop) and
+// 64-k stages measured slower; the 64-k configuration serves K % 128 == 64.
+struct Cfg {
+  int bmb, bnb, bk, occ;
+  double cost;
 };
-constexpr Shape kShapes[] = {{4, 4, 1.00}, {4, 3, 1.10}, {4, 2, 1.28}};
+constexpr Cfg kCfgs[] = {
+    {4, 4, 128, 1, 1.00}, {4, 3, 128, 1, 1.05}, {4, 2, 128, 1, 1.10}, {4, 2, 64, 1, 1.10},
+};
+constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
-template <int DT, int BMB, int BNB, int BK>
+template <int DT, int BMB, int BNB, int BK, int OCC>
 static void launch_tiles(const W8A8Args &a, hipStream_t s) {
-  using G = Tile<BMB, BNB, BK>;
+  using G = Tile<BMB, BNB, BK, OCC>;
   // Rows of xq (multiple of BM) and of w (multiple of BN) per launch, so that
   // the 31-bit copy offsets never overflow.
   const int64_t mc = std::max<int64_t>(G::BM, ((int64_t)((COPY_SPAN - a.K) / a.ldxq) + 1) / G::BM * G::BM);
@@ -427,10 +488,11 @@ static void launch_tiles(const W8A8Args &a, hipStream_t s) {
       const int64_t Mi = std::min(mc, a.M - ms), Ni = std::min(nc, a.N - ns);
       const int tiles_m = (int)((Mi + G::BM - 1) / G::BM), tiles_n = (int)((Ni + G::BN - 1) / G::BN);
       const void *bi = a.bias ? static_cast<const void *>(static_cast<const char *>(a.bias) + ns * bias_sz) : nullptr;
-      hipLaunchKernelGGL((w8a8_gemm_kernel<DT, BMB, BNB, BK>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0,
-                         s, a.xq + ms * a.ldxq, a.ldxq, static_cast<const uint16_t *>(a.xs) + ms, a.w + ns * a.ldw,
-                         a.ldw, a.scale + ns, bi, a.bias_dt, static_cast<uint16_t *>(a.y) + ms * a.ldy + ns, a.ldy,
-                         (int)Mi, (int)Ni, (int)a.K, tiles_m, tiles_n);
+      hipLaunchKernelGGL((w8a8_gemm_kernel<DT, BMB, BNB, BK, OCC>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256),
+                         0, s, a.xq + ms * a.ldxq, a.ldxq, static_cast<const uint16_t *>(a.xs) + ms,
+                         a.w + ns * a.ldw, a.ldw, a.scale + ns, bi, a.bias_dt,
+                         static_cast<uint16_t *>(a.y) + ms * a.ldy + ns, a.ldy, (int)Mi, (int)Ni, (int)a.K, tiles_m,
+                         tiles_n);
     }
 }
 
@@ -442,34 +504,58 @@ static int device_cus() {
   return cus;
 }
 
-// One workgroup per CU (the stages fill the LDS), so tiles run in rounds of
-// `cus`; the shape with the least (rounds x tile area x relative cost) wins.
+template <int DT, int I = 0>
+static void launch_cfg(int idx, const W8A8Args &a, hipStream_t s) {
+  if constexpr (I < kNumCfgs) {
+    constexpr Cfg c = kCfgs[I];
+    if (idx == I) return launch_tiles<DT, c.bmb, c.bnb, c.bk, c.occ>(a, s);
+    launch_cfg<DT, I + 1>(idx, a, s);
+  }
+}
+
+// Tiles run in rounds of (CUs x workgroups per CU); the configuration with
+// the least (rounds x tile area x relative cost) wins.
 template <int DT>
 static void launch_dt(const W8A8Args &a, hipStream_t s) {
   const int cus = device_cus();
-  int pick = 2;
+  int pick = -1;
   double best_t = 0;
-  for (int i = 0; i < 3; ++i) {
-    const Shape &c = kShapes[i];
-    const int64_t bm = 64 * c.bmb, bn = 64 * c.bnb;
+  for (int i = 0; i < kNumCfgs; ++i) {
+    const Cfg &c = kCfgs[i];
+    if (a.K % c.bk != 0 || (c.bk == 64 && a.K % 128 == 0)) continue;
+    const int64_t bm = 64 * c.bmb, bn = 64 * c.bnb, slots = (int64_t)cus * c.occ;
     const int64_t tiles = ((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn);
-    const double t = (double)((tiles + cus - 1) / cus) * (double)(bm * bn) * c.cost;
-    if (i == 0 || t < best_t) pick = i, best_t = t;
+    const double t = (double)((tiles + slots - 1) / slots) * (double)(bm * bn) * c.cost / c.occ;
+    if (pick < 0 || t < best_t) pick = i, best_t = t;
   }
-  bool deep = false;  // 128-k tiles
 #ifdef RA_TUNING
-  if (g_w8a8_mode) pick = g_w8a8_mode % 10 - 1, deep = g_w8a8_mode > 10;
+  if (g_w8a8_mode > 0 && g_w8a8_mode <= kNumCfgs) pick = g_w8a8_mode - 1;
 #endif
-  if (deep) {
-    if (pick == 0) return launch_tiles<DT, 4, 4, 128>(a, s);
-    if (pick == 1) return launch_tiles<DT, 4, 3, 128>(a, s);
-    return launch_tiles<DT, 4, 2, 128>(a, s);
-  }
-  if (pick == 0) return launch_tiles<DT, 4, 4, 64>(a, s);
-  if (pick == 1) return launch_tiles<DT, 4, 3, 64>(a, s);
-  launch_tiles<DT, 4, 2, 64>(a, s);
+  launch_cfg<DT>(pick, a, s);
 }
 
+}  // namespace w8a8
+
+namespace w8a8 {
+template <int DT>
+static bool quantize_act_vec(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, int8_t *q, int64_t ldq,
+                             uint16_t *xs, hipStream_t s) {
+  if (K % 8 != 0 || ldx % 8 != 0 || ldq % 8 != 0 || (reinterpret_cast<uintptr_t>(x) & 15) ||
+      (reinterpret_cast<uintptr_t>(q) & 7))
+    return false;
+  const dim3 grid((unsigned)M), block(kRowThreads);
+  const int64_t per = 8 * kRowThreads;  // elements per chunk slot
+  if (K <= per) hipLaunchKernelGGL((quantize_act_vec_kernel<DT, 1>), grid, block, 0, s, x, ldx, (int)K, q, ldq, xs);
+  else if (K <= 2 * per)
+    hipLaunchKernelGGL((quantize_act_vec_kernel<DT, 2>), grid, block, 0, s, x, ldx, (int)K, q, ldq, xs);
+  else if (K <= 4 * per)
+    hipLaunchKernelGGL((quantize_act_vec_kernel<DT, 4>), grid, block, 0, s, x, ldx, (int)K, q, ldq, xs);
+  else if (K <= 8 * per)
+    hipLaunchKernelGGL((quantize_act_vec_kernel<DT, 8>), grid, block, 0, s, x, ldx, (int)K, q, ldq, xs);
+  else
+    return false;
+  return true;
+}
 }  // namespace w8a8
 
 hipError_t quantize_act_launch(const void *x, int64_t ldx, int x_dt, int64_t M, int64_t K, int8_t *q, int64_t ldq,
@@ -477,6 +563,9 @@ hipError_t quantize_act_launch(const void *x, int64_t ldx, int x_dt, int64_t M, 
   const dim3 grid((unsigned)M), block(w8a8::kRowThreads);
   const uint16_t *xp = static_cast<const uint16_t *>(x);
   uint16_t *sp = static_cast<uint16_t *>(xs);
+  const bool vec = x_dt == RA_F16 ? w8a8::quantize_act_vec<RA_F16>(xp, ldx, M, K, q, ldq, sp, s)
+                                  : w8a8::quantize_act_vec<RA_BF16>(xp, ldx, M, K, q, ldq, sp, s);
+  if (vec) return hipGetLastError();
   if (x_dt == RA_F16)
     hipLaunchKernelGGL((w8a8::quantize_act_kernel<RA_F16>), grid, block, 0, s, xp, ldx, (int)K, q, ldq, sp);
   else
@@ -485,7 +574,7 @@ hipError_t quantize_act_launch(const void *x, int64_t ldx, int x_dt, int64_t M, 
 }
 
 bool w8a8_tiled_supported(const W8A8Args &a) {
-  if (a.K % 128 != 0 || a.K == 0) return false;
+  if (a.K % 64 != 0 || a.K == 0) return false;
   if ((reinterpret_cast<uintptr_t>(a.xq) & 15) || (reinterpret_cast<uintptr_t>(a.w) & 15)) return false;
   if (a.ldxq % 16 != 0 || a.ldw % 16 != 0) return false;
   if ((uint64_t)(255 * a.ldxq + a.K) > w8a8::COPY_SPAN || (uint64_t)(255 * a.ldw + a.K) > w8a8::COPY_SPAN)

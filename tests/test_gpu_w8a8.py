@@ -50,7 +50,7 @@ def _np(t):
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("M,K", [(1, 128), (5, 7), (17, 4096), (300, 200), (64, 11008), (9, 8192)])
+@pytest.mark.parametrize("M,K", [(1, 128), (5, 7), (17, 4096), (300, 200), (64, 11008), (9, 8192), (3, 16392)])
 def test_quantize_activations_bit_exact(gpu, dt, M, K):
     print(f"  act-quant M={M} K={K} dt={dt}", flush=True)
     x = _acts(M, K, dt, seed=M + K)
@@ -74,10 +74,11 @@ def test_quantize_activations_strided_rows(gpu):
     np.testing.assert_array_equal(_np(xs), xs_ref)
 
 
-# (M, N, K): K % 128 == 0 runs the MFMA kernel (ragged M / N, every tile
-# shape), the others the any-K kernel.
+# (M, N, K): K % 64 == 0 runs the MFMA kernel (ragged M / N, every tile
+# shape; K % 128 == 64 the 64-k stages), the others the any-K kernel.
 GEMM_SHAPES = [(17, 128, 128), (64, 256, 96), (300, 320, 256), (256, 192, 512), (513, 129, 1024),
-               (1000, 64, 128), (256, 256, 384), (1024, 1024, 256), (33, 50, 200), (40, 70, 136)]
+               (1000, 64, 128), (256, 256, 384), (1024, 1024, 256), (300, 200, 192), (64, 256, 320),
+               (33, 50, 200), (40, 70, 136)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
