@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define RA_ABI_VERSION 3
+#define RA_ABI_VERSION 4
 
 enum ra_dtype { RA_F16 = 0, RA_BF16 = 1, RA_F32 = 2 };
 
@@ -144,6 +144,17 @@ int ra_rmsnorm_residual(const void *x, int64_t ldx, int x_dtype,
  */
 int ra_swiglu(const void *gate, const void *up, void *out, int64_t n,
               int dtype, void *stream);
+
+/*
+ * out = silu(gate + bias_gate[i % hidden]) * (up + bias_up[i % hidden]) over
+ * n = rows * hidden contiguous elements (dtype), biases [hidden] in
+ * bias_dtype; fp32 math, one rounding. Replaces swiglu_with_bias
+ * (src/rotalabs_accel/kernels/swiglu.py:221-260 -> _swiglu_fused_kernel_with_bias
+ * :180-218).
+ */
+int ra_swiglu_bias(const void *gate, const void *up,
+                   const void *bias_gate, const void *bias_up, int bias_dtype,
+                   void *out, int64_t n, int64_t hidden, int dtype, void *stream);
 
 /*
  * Per-output-channel symmetric int8 quantization of w[N,K] (w_dtype RA_F32,

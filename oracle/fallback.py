@@ -13,6 +13,8 @@ uses the same ops, on CPU tensors only:
                    = the same on v = (x + residual).float(), rounded to x.dtype
   swiglu_torch     src/rotalabs_accel/kernels/activations.py:36-45
                    = silu(gate) * up
+  swiglu_with_bias src/rotalabs_accel/kernels/swiglu.py:221-260
+                   = (silu(gate.f32 + bg.f32) * (up.f32 + bu.f32)).to(gate.dtype)
 
 plus ``mlp_ref`` (RMSNorm -> gate/up -> SwiGLU -> down, the decoder-MLP
 composition of the reference's SwiGLU module, activations.py:141-178, with
@@ -68,6 +70,23 @@ def quantized_tensor_ref(t: torch.Tensor, bits: int = 8, per_channel: bool = Tru
 def swiglu_ref(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """activations.py:36-45 on CPU tensors."""
     return F.silu(gate) * up
+
+
+def swiglu_with_bias_ref(gate: torch.Tensor, up: torch.Tensor, bias_gate: torch.Tensor,
+                         bias_up: torch.Tensor) -> torch.Tensor:
+    """swiglu_with_bias (src/rotalabs_accel/kernels/swiglu.py:221-260): its
+    Triton kernel (:201-218) loads gate, up and both biases as fp32, adds,
+    computes silu(g) * u in fp32 and rounds once to gate's dtype."""
+    g = gate.float() + bias_gate.float()
+    u = up.float() + bias_up.float()
+    return (F.silu(g) * u).to(gate.dtype)
+
+
+def swiglu_with_bias_f64(gate: np.ndarray, up: np.ndarray, bias_gate: np.ndarray, bias_up: np.ndarray):
+    """float64 closed form of the same, for pinning the restatement."""
+    g = gate.astype(np.float64) + bias_gate.astype(np.float64)[None, :]
+    u = up.astype(np.float64) + bias_up.astype(np.float64)[None, :]
+    return g / (1.0 + np.exp(-g)) * u
 
 
 def swiglu_ffn_ref(x, q_gu, s_gu, q_down, s_down, b_gu=None, b_down=None):

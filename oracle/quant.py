@@ -61,6 +61,8 @@ def quantize_symmetric(t32: np.ndarray, dtype: str = "f32", dim: int | None = No
       scale   = 1 where scale == 0              (:70)
       q       = int8(clamp(rne(round(t / scale)), -128, 127))   (:73)
       scale   = scale.float(); squeeze(dim)     (:76-80)
+    NaN propagates through the amax (a row holding NaN gets a NaN scale) and a
+    NaN quotient converts to 0, as torch's CPU conversion does.
     """
     t32 = np.asarray(t32, dtype=np.float32)
     a = np.abs(t32)
@@ -71,8 +73,10 @@ def quantize_symmetric(t32: np.ndarray, dtype: str = "f32", dim: int | None = No
         max_val = a.max(axis=dim, keepdims=True)
     scale = round_to(np.asarray(max_val / np.float32(QMAX), dtype=np.float32), dtype)
     scale = np.where(scale == 0, np.float32(1.0), scale).astype(np.float32)
-    ratio = round_to((t32 / scale).astype(np.float32), dtype)
-    q = np.clip(np.rint(ratio), -128, 127).astype(np.int8)
+    with np.errstate(invalid="ignore"):
+        ratio = round_to((t32 / scale).astype(np.float32), dtype)
+    r = np.rint(ratio)
+    q = np.where(np.isnan(r), 0, np.clip(r, -128, 127)).astype(np.int8)
     scale = scale.astype(np.float32)
     if dim is not None:
         scale = np.squeeze(scale, axis=dim)

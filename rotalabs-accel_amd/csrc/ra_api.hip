@@ -190,6 +190,16 @@ int ra_swiglu(const void *gate, const void *up, void *out, int64_t n, int dtype,
   return to_status(swiglu_launch(gate, up, out, n, dtype, static_cast<hipStream_t>(stream)));
 }
 
+int ra_swiglu_bias(const void *gate, const void *up, const void *bias_gate, const void *bias_up, int bias_dtype,
+                   void *out, int64_t n, int64_t hidden, int dtype, void *stream) {
+  if (n < 0 || hidden <= 0 || n % hidden != 0) return RA_ERR_ARG;
+  if (!valid_act(dtype) || !valid_act(bias_dtype)) return RA_ERR_DTYPE;
+  if (n == 0) return RA_OK;
+  if (!gate || !up || !out || !bias_gate || !bias_up) return RA_ERR_ARG;
+  return to_status(swiglu_bias_launch(gate, up, bias_gate, bias_up, bias_dtype, out, n, hidden, dtype,
+                                      static_cast<hipStream_t>(stream)));
+}
+
 int ra_quantize_per_channel(const void *w, int64_t ldw, int w_dtype, int64_t N, int64_t K, int8_t *q,
                             int64_t ldq, float *scale, void *stream) {
   if (N < 0 || K < 0 || N > INT32_MAX || K > INT32_MAX) return RA_ERR_ARG;

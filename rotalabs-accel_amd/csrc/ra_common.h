@@ -23,6 +23,16 @@ __device__ __forceinline__ void store8(void *p, uint32_t lo, uint32_t hi) {
   *reinterpret_cast<u32x2_t *>(p) = u32x2_t{lo, hi};
 }
 
+// v as an fp32 register value: the backend otherwise folds an fp32 result
+// feeding a 16-bit conversion into one mixed-precision FMA (v_fma_mix),
+// which rounds once instead of to fp32 first and then to 16 bits. (volatile:
+// the value is also computed where it is written, not sunk into a later
+// conditional block.)
+__device__ __forceinline__ float fp32_rounded(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [LO, HI).
 template <int LO, int HI, typename F>
 __device__ __forceinline__ void static_for_int(F &&f) {
@@ -184,6 +194,14 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += dpp_moved<0x142, 0xA>(v);  // row_bcast15 into rows 1 and 3
   v += dpp_moved<0x143, 0xC>(v);  // row_bcast31 into rows 2 and 3
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// NaN-propagating maximum (torch's amax semantics; v_maximum*_f32 on gfx950).
+__device__ __forceinline__ float nan_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float wave_maximum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = nan_max(v, __shfl_xor(v, off, 64));
+  return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {

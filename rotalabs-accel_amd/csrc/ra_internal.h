@@ -79,6 +79,8 @@ hipError_t rmsnorm_launch(const void *x, int64_t ldx, int x_dt, const void *r, i
                           const void *w, int w_dt, void *y, int64_t ldy, int y_dt, int64_t rows, int64_t hidden,
                           float eps, hipStream_t s);
 hipError_t swiglu_launch(const void *g, const void *u, void *o, int64_t n, int dt, hipStream_t s);
+hipError_t swiglu_bias_launch(const void *g, const void *u, const void *bg, const void *bu, int b_dt, void *o,
+                              int64_t n, int64_t hidden, int dt, hipStream_t s);
 hipError_t quantize_launch(const void *w, int64_t ldw, int w_dt, int64_t N, int64_t K, int8_t *q,
                            int64_t ldq, float *scale, hipStream_t s);
 hipError_t quantize_rows_launch(const void *t, int64_t ldt, int t_dt, int64_t rows, int64_t cols, int bits,

@@ -11,15 +11,16 @@ namespace ra {
 
 constexpr int kRowThreads = 256;
 
+// Workgroup sum, or NaN-propagating maximum (as torch's amax).
 template <bool IsMax>
 __device__ __forceinline__ float block_reduce(float v, float *smem) {
-  v = IsMax ? wave_max(v) : wave_sum(v);
+  v = IsMax ? wave_maximum(v) : wave_sum(v);
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   if (lane == 0) smem[wid] = v;
   __syncthreads();
   float r = smem[0];
 #pragma unroll
-  for (int i = 1; i < kRowThreads / 64; ++i) r = IsMax ? fmaxf(r, smem[i]) : r + smem[i];
+  for (int i = 1; i < kRowThreads / 64; ++i) r = IsMax ? nan_max(r, smem[i]) : r + smem[i];
   return r;
 }
 
@@ -169,12 +170,39 @@ hipError_t swiglu_launch(const void *g, const void *u, void *o, int64_t n, int d
   return hipGetLastError();
 }
 
+// out = silu(g + bg) * (u + bu) in fp32, one rounding, bias index i % hidden
+// (the arithmetic of swiglu_with_bias's Triton kernel,
+// src/rotalabs_accel/kernels/swiglu.py:201-218).
+__global__ __launch_bounds__(256) void swiglu_bias_kernel(const void *__restrict__ g, const void *__restrict__ u,
+                                                          const void *__restrict__ bg, const void *__restrict__ bu,
+                                                          int b_dt, void *__restrict__ o, int64_t n, int64_t hidden,
+                                                          int dt) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t c = i % hidden;
+    const float gv = load_as_f32(g, i, dt) + load_as_f32(bg, c, b_dt);
+    const float uv = load_as_f32(u, i, dt) + load_as_f32(bu, c, b_dt);
+    store_from_f32(o, i, dt, gv / (1.0f + expf(-gv)) * uv);
+  }
+}
+
+hipError_t swiglu_bias_launch(const void *g, const void *u, const void *bg, const void *bu, int b_dt, void *o,
+                              int64_t n, int64_t hidden, int dt, hipStream_t s) {
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(swiglu_bias_kernel, dim3((unsigned)blocks), dim3(256), 0, s, g, u, bg, bu, b_dt, o, n, hidden,
+                     dt);
+  return hipGetLastError();
+}
+
 // Per-row symmetric quantisation, the op sequence of quantize_symmetric(dim=1)
 // (src/rotalabs_accel/quantization/symmetric.py:66-80) on the CPU:
 //   s = round_w(amax / 127)   IEEE division (built without fast-math)
 //   s = 1 if s == 0
 //   q = int8(clamp(rint(round_w(w / s)), -128, 127))   rint: half to even
-// round_w is the rounding to the weight dtype (identity for fp32).
+// round_w is the rounding to the weight dtype (identity for fp32). amax
+// propagates NaN (torch's amax) and a NaN quotient converts to 0, as the CPU
+// conversion does.
 __global__ __launch_bounds__(kRowThreads) void quantize_kernel(const void *__restrict__ w, int64_t ldw,
                                                                int w_dt, int K, int8_t *__restrict__ q,
                                                                int64_t ldq, float *__restrict__ scale) {
@@ -182,14 +210,13 @@ __global__ __launch_bounds__(kRowThreads) void quantize_kernel(const void *__res
   const int64_t row = blockIdx.x;
   float amax = 0.f;
   for (int i = threadIdx.x; i < K; i += kRowThreads)
-    amax = fmaxf(amax, fabsf(load_as_f32(w, row * ldw + i, w_dt)));
+    amax = nan_max(amax, fabsf(load_as_f32(w, row * ldw + i, w_dt)));
   amax = block_reduce<true>(amax, smem);
   float s = round_through(amax / 127.0f, w_dt);
   if (s == 0.0f) s = 1.0f;
   for (int i = threadIdx.x; i < K; i += kRowThreads) {
-    const float v = round_through(load_as_f32(w, row * ldw + i, w_dt) / s, w_dt);
-    const float rq = fminf(fmaxf(rintf(v), -128.0f), 127.0f);
-    q[row * ldq + i] = (int8_t)(int)rq;
+    const float v = rintf(round_through(load_as_f32(w, row * ldw + i, w_dt) / s, w_dt));
+    q[row * ldq + i] = v != v ? (int8_t)0 : (int8_t)(int)fminf(fmaxf(v, -128.0f), 127.0f);
   }
   if (threadIdx.x == 0) scale[row] = s;
 }
@@ -216,9 +243,9 @@ __global__ __launch_bounds__(kRowThreads) void quantize_rows_kernel(const void *
   const int64_t row = blockIdx.x;
   float amax = 0.f;
   for (int i = threadIdx.x; i < cols; i += kRowThreads)
-    amax = fmaxf(amax, fabsf(load_as_f32(t, row * ldt + i, t_dt)));
+    amax = nan_max(amax, fabsf(load_as_f32(t, row * ldt + i, t_dt)));
   amax = block_reduce<true>(amax, smem);
-  const float s = round_through(fmaxf(round_through(amax / (float)qmax, t_dt), 1e-8f), t_dt);
+  const float s = round_through(nan_max(round_through(amax / (float)qmax, t_dt), 1e-8f), t_dt);
   for (int i = threadIdx.x; i < cols; i += kRowThreads) {
     const float v = round_through(load_as_f32(t, row * ldt + i, t_dt) / s, t_dt);
     const float r = rintf(v);
@@ -245,6 +272,7 @@ __global__ __launch_bounds__(256) void quantize_rows_short_kernel(const uint16_t
   const int c = lane % L;                    // 16-byte chunk of this lane
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + wid) * (RPW * U) + lane / L;
   const int cc = 8 * c < cols ? c : 0;       // clamped: loads stay unconditional
+  const float qf = (float)qmax, rq = 1.0f / qf, qlo = -qf - 1.0f, qhi = qf;
   uint4 v[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -261,18 +289,36 @@ __global__ __launch_bounds__(256) void quantize_rows_short_kernel(const uint16_t
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       x[e] = A::in(h[e]);
-      amax = fmaxf(amax, fabsf(x[e]));
+      amax = nan_max(amax, fabsf(x[e]));  // NaN propagates, as torch's amax
     }
     if (!live) amax = 0.f;
 #pragma unroll
-    for (int off = L / 2; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-    const float sc = A::rnd(fmaxf(A::rnd(amax / (float)qmax), 1e-8f));
+    for (int off = L / 2; off >= 1; off >>= 1) amax = nan_max(amax, __shfl_xor(amax, off, 64));
+    // amax / qmax by the same correction (exact for every finite 16-bit amax
+    // and qmax = 127 or 7, checked exhaustively; inf and NaN pass through)
+    const float d0 = amax * rq;
+    const float d = __builtin_isfinite(d0) ? __builtin_fmaf(__builtin_fmaf(-d0, qf, amax), rq, d0) : d0;
+    const float sc = A::rnd(nan_max(A::rnd(fp32_rounded(d)), 1e-8f));
     if (!live) continue;
+    // x / sc correctly rounded to fp32 without a division per element:
+    // Markstein's correction of x * RN(1/sc) by one residual FMA. For every
+    // 16-bit x and 16-bit sc >= 1e-8 with |x / sc| <= 256 (the codec's range:
+    // |x| <= amax, sc ~ amax / qmax) it rounds to the same 16-bit value as the
+    // IEEE quotient (checked exhaustively on the CPU, both formats). A zero
+    // scale (fp16 rounds the 1e-8 floor to 0) or an infinite one (a row
+    // holding inf) keeps the plain product x * (1 / sc): +-inf / NaN for
+    // x / 0, 0 / NaN for x / inf, as the quotient.
+    const float rinv = 1.0f / sc;
+    const bool correct = sc != 0.0f && __builtin_isfinite(sc);
     uint32_t lo = 0, hi = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float r = rintf(A::rnd(x[e] / sc));
-      const int qi = r != r ? 0 : (int)fminf(fmaxf(r, (float)(-qmax - 1)), (float)qmax);
+      const float q0 = x[e] * rinv;
+      const float q1 = correct ? __builtin_fmaf(__builtin_fmaf(-q0, sc, x[e]), rinv, q0) : q0;
+      // (the rounded value goes through a register again: otherwise the
+      // compiler re-rounds the integral rint result to 16 bits)
+      const float r = rintf(fp32_rounded(A::rnd(fp32_rounded(q1))));
+      const int qi = r != r ? 0 : (int)__builtin_amdgcn_fmed3f(r, qlo, qhi);
       const uint32_t b = (uint32_t)(uint8_t)(int8_t)qi;
       if (e < 4) lo |= b << (8 * e);
       else hi |= b << (8 * (e - 4));

@@ -42,37 +42,23 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kRowThreads = 256;
 
-// v as an fp32 register value: the backend otherwise folds a product feeding
-// a 16-bit conversion into one mixed-precision FMA (v_fma_mix), which rounds
-// once instead of to fp32 first and then to 16 bits.
-__device__ __forceinline__ float fp32_rounded(float v) {
-  asm volatile("" : "+v"(v));
-  return v;
-}
-
 template <int DT>
 __global__ __launch_bounds__(kRowThreads) void quantize_act_kernel(const uint16_t *__restrict__ x, int64_t ldx,
                                                                    int K, int8_t *__restrict__ q, int64_t ldq,
                                                                    uint16_t *__restrict__ xs) {
   using A = Act<DT>;
-  __shared__ float smem[2][kRowThreads / 64];
+  __shared__ float smem[kRowThreads / 64];
   const int64_t row = blockIdx.x;
   const uint16_t *xr = x + row * ldx;
-  float amax = 0.f, nan = 0.f;  // amax propagates NaN like torch's amax: tracked as a flag
-  for (int i = threadIdx.x; i < K; i += kRowThreads) {
-    const float v = A::in(xr[i]);
-    amax = fmaxf(amax, fabsf(v));
-    nan = v != v ? 1.f : nan;
-  }
-  amax = wave_max(amax);
-  nan = wave_max(nan);
-  if ((threadIdx.x & 63) == 0) smem[0][threadIdx.x >> 6] = amax, smem[1][threadIdx.x >> 6] = nan;
+  float amax = 0.f;  // NaN propagates, as torch's amax
+  for (int i = threadIdx.x; i < K; i += kRowThreads) amax = nan_max(amax, fabsf(A::in(xr[i])));
+  amax = wave_maximum(amax);
+  if ((threadIdx.x & 63) == 0) smem[threadIdx.x >> 6] = amax;
   __syncthreads();
-  amax = fmaxf(fmaxf(smem[0][0], smem[0][1]), fmaxf(smem[0][2], smem[0][3]));
-  nan = fmaxf(fmaxf(smem[1][0], smem[1][1]), fmaxf(smem[1][2], smem[1][3]));
-  // clamp(min=1e-5) compares against the bound rounded to the tensor dtype;
-  // 127 / a is torch's reciprocal(a) * 127, each rounded.
-  const float a = nan != 0.f ? __builtin_nanf("") : fmaxf(amax, A::rnd(1e-5f));
+  amax = nan_max(nan_max(smem[0], smem[1]), nan_max(smem[2], smem[3]));
+  // clamp(min=1e-5) compares against the bound rounded to the tensor dtype
+  // (and keeps NaN); 127 / a is torch's reciprocal(a) * 127, each rounded.
+  const float a = nan_max(amax, A::rnd(1e-5f));
   const float mult = A::rnd(A::rnd(1.0f / a) * 127.0f);
   for (int i = threadIdx.x; i < K; i += kRowThreads) {
     const float r = rintf(A::rnd(A::in(xr[i]) * mult));
@@ -89,12 +75,12 @@ __global__ __launch_bounds__(kRowThreads) void quantize_act_vec_kernel(const uin
                                                                        int K, int8_t *__restrict__ q, int64_t ldq,
                                                                        uint16_t *__restrict__ xs) {
   using A = Act<DT>;
-  __shared__ float smem[2][kRowThreads / 64];
+  __shared__ float smem[kRowThreads / 64];
   const int64_t row = blockIdx.x;
   const uint4 *xr = reinterpret_cast<const uint4 *>(x + row * ldx);
   const int chunks = K >> 3;
   uint4 v[NC];
-  float amax = 0.f, nan = 0.f;
+  float amax = 0.f;
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
     const int c = threadIdx.x + j * kRowThreads;
@@ -102,18 +88,14 @@ __global__ __launch_bounds__(kRowThreads) void quantize_act_vec_kernel(const uin
     const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
     for (int h = 0; h < 8; ++h) {
-      const float f = A::in((uint16_t)(w[h >> 1] >> (16 * (h & 1))));
-      amax = fmaxf(amax, fabsf(f));
-      nan = f != f ? 1.f : nan;
+      amax = nan_max(amax, fabsf(A::in((uint16_t)(w[h >> 1] >> (16 * (h & 1))))));
     }
   }
-  amax = wave_max(amax);
-  nan = wave_max(nan);
-  if ((threadIdx.x & 63) == 0) smem[0][threadIdx.x >> 6] = amax, smem[1][threadIdx.x >> 6] = nan;
+  amax = wave_maximum(amax);
+  if ((threadIdx.x & 63) == 0) smem[threadIdx.x >> 6] = amax;
   __syncthreads();
-  amax = fmaxf(fmaxf(smem[0][0], smem[0][1]), fmaxf(smem[0][2], smem[0][3]));
-  nan = fmaxf(fmaxf(smem[1][0], smem[1][1]), fmaxf(smem[1][2], smem[1][3]));
-  const float a = nan != 0.f ? __builtin_nanf("") : fmaxf(amax, A::rnd(1e-5f));
+  amax = nan_max(nan_max(smem[0], smem[1]), nan_max(smem[2], smem[3]));
+  const float a = nan_max(amax, A::rnd(1e-5f));
   const float mult = A::rnd(A::rnd(1.0f / a) * 127.0f);
   int8_t *qr = q + row * ldq;
 #pragma unroll
@@ -263,7 +245,7 @@ __device__ __forceinline__ void epilogue(const i32x16 (&acc)[BMB][BNB], const ui
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
-  const bool guard = rows_left < 32 * BMB + 4;  // some row of this wave is past M
+  const bool guard = rows_left < 32 * BMB - 4;  // some row r <= 32 * BMB - 5 of this lane is past M
   if (bias) {
     if (guard) store_blocks(T_{}, T_{});
     else store_blocks(F_{}, T_{});

@@ -331,3 +331,22 @@ def test_w8a8_route_cpu_matches_oracle(tdt, dt):
     torch.testing.assert_close(small, ra.int8_gemm(x[:, :8], q, s, b), rtol=0, atol=0)
     with pytest.raises(ValueError):
         qm.quantize_activations(x, act_scale=100.0)
+
+
+def test_swiglu_module_and_bias_cpu():
+    """kernels.swiglu (swiglu.py:79-260): the activation-only SwiGLU module and
+    swiglu_with_bias on CPU tensors equal the oracle; the reference's asserts."""
+    from rotalabs_accel.kernels import swiglu as sw
+    g = torch.Generator().manual_seed(2)
+    gate = torch.randn(2, 3, 64, generator=g).half()
+    up = torch.randn(2, 3, 64, generator=g).half()
+    assert torch.equal(sw.SwiGLU()(gate, up), fallback.swiglu_ref(gate, up))
+    bg = torch.randn(64, generator=g).half()
+    bu = torch.randn(64, generator=g).float()
+    y = sw.swiglu_with_bias(gate, up, bg, bu)
+    assert y.dtype == torch.float16 and y.shape == gate.shape
+    assert torch.equal(y, fallback.swiglu_with_bias_ref(gate, up, bg, bu))
+    with pytest.raises(AssertionError):
+        sw.swiglu_with_bias(gate, up[..., :32], bg, bu)
+    with pytest.raises(AssertionError):
+        sw.swiglu_with_bias(gate, up, bg[:32], bu)

@@ -31,11 +31,29 @@ def test_quantize_fp32_bit_exact(gpu):
     w[1, :9] = torch.tensor([127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -125.5])
     w[2] *= 1e-35                      # subnormal scales
     w[3] = torch.linspace(-3, 3, 1000)
+    w[4, 17] = float("nan")            # NaN scale, q = 0 (torch's amax and conversion)
     print("  quantize fp32 [300,1000]", flush=True)
     q, s = ra.quantize_weight_per_channel(w.to(gpu))
     q_o, s_o = oq.quantize_weight_per_channel(w.numpy())
     assert np.array_equal(q.cpu().numpy(), q_o)
-    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_o.view(np.uint32))
+    keep = np.arange(300) != 4
+    assert np.array_equal(s.cpu().numpy()[keep].view(np.uint32), s_o[keep].view(np.uint32))
+    assert np.isnan(s.cpu().numpy()[4]) and np.isnan(s_o[4])
+
+
+@pytest.mark.parametrize("dt,name", [(torch.float16, "f16"), (torch.bfloat16, "bf16")])
+def test_quantize_reduced_edge_rows(gpu, dt, name):
+    """16-bit weights with a zero row, a NaN row and a constant row vs the oracle."""
+    g = torch.Generator().manual_seed(9)
+    w = (torch.randn(6, 520, generator=g) * 0.05).to(dt)
+    w[0] = 0
+    w[2, 100] = float("nan")
+    w[3] = 0.25
+    print(f"  quantize {dt} edge rows", flush=True)
+    q, s = ra.quantize_weight_per_channel(w.to(gpu))
+    q_o, s_o = oq.quantize_weight_per_channel(w.float().numpy(), name)
+    assert np.array_equal(q.cpu().numpy(), q_o)
+    assert np.array_equal(s.cpu().numpy(), s_o, equal_nan=True)
 
 
 @pytest.mark.parametrize("name,dt", [("f16", torch.float16), ("bf16", torch.bfloat16)])
@@ -157,13 +175,27 @@ def test_kv_codec_rows_bit_exact(gpu, dt, bits, cols):
     t = (torch.randn(3, 8, 37, cols, generator=g) * 4).to(dt)
     t[0, 0, 0] = 0
     t[1, 2, 5, :] = 2.5
-    print(f"  kv codec {dt} bits={bits}", flush=True)
+    # edge rows: NaN (propagates into the scale, q = 0), tiny and huge
+    # magnitudes, and exact ties of the quotient: with amax = qmax / 8 the
+    # scale is 1/8 and (k + 1/2) / 8 divides to k + 1/2
+    t[2, 3, 0, cols // 2] = float("nan")
+    t[2, 3, 1] = torch.randn(cols, generator=g) * (1e-6 if dt == torch.float16 else 1e-30)
+    t[2, 3, 2] = torch.randn(cols, generator=g) * (3e4 if dt == torch.float16 else 1e37)
+    qm = 2 ** (bits - 1) - 1
+    ties = (torch.arange(cols) % (2 * qm) - qm + 0.5) / 8
+    ties[0] = qm / 8
+    t[2, 3, 3] = ties.to(dt)
+    print(f"  kv codec {dt} bits={bits} cols={cols}", flush=True)
     qt = QuantizedTensor(t.to(gpu), bits=bits)
     q, s = fallback.quantized_tensor_ref(t, bits)
     assert qt.data.shape == t.shape and qt.scale.shape == t.shape[:-1] + (1,)
     assert qt.scale.dtype == dt
-    assert torch.equal(qt.data.cpu(), q) and torch.equal(qt.scale.cpu(), s)
-    assert torch.equal(qt.dequantize().cpu(), q.to(dt) * s)
+    assert torch.equal(qt.data.cpu(), q)
+    assert torch.equal(qt.scale.cpu().isnan(), s.isnan()) and s[2, 3, 0].isnan().all()
+    fin = ~s.isnan()
+    assert torch.equal(qt.scale.cpu()[fin], s[fin])
+    # (0 * inf of a row holding inf is NaN on both sides)
+    torch.testing.assert_close(qt.dequantize().cpu(), q.to(dt) * s, rtol=0, atol=0, equal_nan=True)
 
 
 def test_rmsnorm_golden(gpu, golden):
@@ -301,3 +333,27 @@ def test_mlp_workload_full_size(gpu, M, H, I, seed):
     mlp.norm_weight.data.copy_(c.norm_w)
     mlp._quantized = True
     assert torch.equal(mlp(c.x), y)
+
+
+@pytest.mark.parametrize("shape,tdt,bdt", [((3, 7, 11008), torch.float16, torch.float16),
+                                           ((5, 4096), torch.bfloat16, torch.float32),
+                                           ((2, 300), torch.float32, torch.bfloat16),
+                                           ((0, 64), torch.float16, torch.float16)])
+def test_swiglu_with_bias_vs_oracle(gpu, shape, tdt, bdt):
+    """ra_swiglu_bias vs the oracle (fp32 math, one rounding): within one
+    output rounding (the fp32 exp differs from the CPU's in the last bits),
+    and within the 1e-2 bar."""
+    from rotalabs_accel.kernels.swiglu import swiglu_with_bias
+    print(f"  swiglu_with_bias shape={shape} dt={tdt} bias={bdt}", flush=True)
+    g = torch.Generator().manual_seed(7)
+    gate = (torch.randn(shape, generator=g) * 3).to(tdt)
+    up = torch.randn(shape, generator=g).to(tdt)
+    bg = torch.randn(shape[-1], generator=g).to(bdt)
+    bu = torch.randn(shape[-1], generator=g).to(bdt)
+    y = swiglu_with_bias(gate.to(gpu), up.to(gpu), bg.to(gpu), bu.to(gpu))
+    torch.cuda.synchronize()
+    ref = fallback.swiglu_with_bias_ref(gate, up, bg, bu)
+    assert y.dtype == tdt and y.shape == gate.shape
+    ulp = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7, torch.float32: 2.0 ** -21}[tdt]
+    torch.testing.assert_close(y.cpu(), ref, rtol=ulp, atol=1e-6)
+    torch.testing.assert_close(y.cpu().float(), ref.float(), rtol=1e-2, atol=1e-2)

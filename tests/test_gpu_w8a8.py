@@ -77,7 +77,7 @@ def test_quantize_activations_strided_rows(gpu):
 # (M, N, K): K % 64 == 0 runs the MFMA kernel (ragged M / N, every tile
 # shape; K % 128 == 64 the 64-k stages), the others the any-K kernel.
 GEMM_SHAPES = [(17, 128, 128), (64, 256, 96), (300, 320, 256), (256, 192, 512), (513, 129, 1024),
-               (1000, 64, 128), (256, 256, 384), (1024, 1024, 256), (300, 200, 192), (64, 256, 320),
+               (1000, 64, 128), (256, 256, 384), (1024, 1024, 256), (300, 200, 192), (64, 256, 320), (252, 192, 256),
                (33, 50, 200), (40, 70, 136)]
 
 

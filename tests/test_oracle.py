@@ -233,12 +233,16 @@ def test_kv_codec_restatements_agree(dtype, bits):
     qmax = 2 ** (bits - 1) - 1
     t[3, 0] = float(qmax)                            # scale 1 (exactly representable)
     t[3, 1:6] = torch.tensor([0.5, 1.5, 2.5, -0.5, -1.5])
+    t[4] = (torch.randn(40, generator=g) * 1e-6).to(tdt)  # fp16: the floored scale rounds to 0 -> +-inf -> clamp
     qt, st = fallback.quantized_tensor_ref(t, bits)
     qn, sn = oq.quantized_tensor_rows(t.float().numpy(), dtype, bits)
     assert np.array_equal(qt.numpy(), qn)
     assert np.array_equal(st.float().numpy(), sn)
     assert qt[3, 1:6].tolist() == [0, 2, 2, 0, -2]  # round half to even
-    assert (qt.abs() <= qmax).all() and (qt[1] == 0).all()
+    assert (qt.int().abs() <= qmax + 1).all() and (qt[1] == 0).all()
+    if dtype == "f16" and bits == 8:     # amax / 127 of a 1e-6 row underflows fp16
+        nz = t[4] != 0
+        assert st[4].item() == 0 and (qt[4][nz].int().abs() >= qmax).all()
     nz = t.abs().amax(dim=-1) > 0
     # the scale rounded to a 16-bit dtype can exceed amax / qmax by half an ulp
     assert (qt.abs().amax(dim=-1)[nz] >= (qmax if dtype == "f32" else qmax - 1)).all()
@@ -323,3 +327,48 @@ def test_w8a8_gemm_oracle_pinned():
     b = oq.round_to(g.uniform(-1, 1, N).astype(np.float32), "bf16")
     y3 = oq.w8a8_gemm_rows(xq, xs, q, s, "f32", b)
     np.testing.assert_array_equal(y3, oq.w8a8_gemm_rows(xq, xs, q, s, "f32") + b[None, :])
+
+
+@pytest.mark.parametrize("tdt", [torch.float16, torch.bfloat16, torch.float32])
+def test_swiglu_with_bias_oracle_pinned(tdt):
+    """swiglu_with_bias_ref (swiglu.py:201-218: fp32 math, one rounding) is
+    within one output rounding of the float64 closed form, with biases that
+    differ per column (a bias indexed by row, or gate / up biases swapped,
+    fails the same bound)."""
+    g = torch.Generator().manual_seed(5)
+    rows, hidden = 6, 96
+    gate = (torch.randn(rows, hidden, generator=g) * 3).to(tdt)
+    up = torch.randn(rows, hidden, generator=g).to(tdt)
+    bg = torch.linspace(-2, 2, hidden).to(tdt)
+    bu = (torch.randn(hidden, generator=g) * 0.5).to(tdt)
+    ref = fallback.swiglu_with_bias_ref(gate, up, bg, bu)
+    assert ref.dtype == tdt
+    exact = fallback.swiglu_with_bias_f64(gate.float().numpy(), up.float().numpy(), bg.float().numpy(),
+                                          bu.float().numpy())
+    ulp = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8, torch.float32: 2.0 ** -23}[tdt]
+    tol = lambda e: np.abs(e) * ulp * 1.01 + 1e-30 + 8 * np.abs(e) * 2.0 ** -24   # one rounding + fp32 noise
+    assert (np.abs(ref.double().numpy() - exact) <= tol(exact)).all()
+    swapped = fallback.swiglu_with_bias_ref(gate, up, bu, bg).double().numpy()
+    assert not (np.abs(swapped - exact) <= tol(exact)).all()
+    by_row = fallback.swiglu_with_bias_ref(gate, up, bg.flip(0), bu).double().numpy()
+    assert not (np.abs(by_row - exact) <= tol(exact)).all()
+
+
+@pytest.mark.parametrize("tdt,dt", [(torch.float32, "f32"), (torch.float16, "f16"), (torch.bfloat16, "bf16")])
+def test_nan_rows_follow_torch(tdt, dt):
+    """Rows holding NaN: torch's amax propagates it (NaN scale) and the NaN
+    quotients convert to 0 on the CPU; the numpy restatements of the weight
+    quantiser, the KV codec and the W8A8 activation quantiser do the same."""
+    from rotalabs_accel.quantization.symmetric import quantize_weight_per_channel
+    g = torch.Generator().manual_seed(8)
+    w = torch.randn(4, 64, generator=g).to(tdt)
+    w[1, 7] = float("nan")
+    q_t, s_t = quantize_weight_per_channel(w)
+    q_o, s_o = oq.quantize_weight_per_channel(w.float().numpy(), dt)
+    assert np.array_equal(q_t.numpy(), q_o) and (q_o[1] == 0).all()
+    assert np.array_equal(s_t.numpy(), s_o, equal_nan=True) and np.isnan(s_o[1])
+    for bits in (8, 4):
+        qt, st = fallback.quantized_tensor_ref(w, bits)
+        qn, sn = oq.quantized_tensor_rows(w.float().numpy(), dt, bits)
+        assert np.array_equal(qt.numpy(), qn) and (qn[1] == 0).all()
+        assert np.array_equal(st.float().numpy(), sn, equal_nan=True) and np.isnan(sn[1]).all()
