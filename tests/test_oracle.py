@@ -8,6 +8,8 @@
 * GEMM: the float64 reference equals a brute-force triple loop (C) and exact
   known answers (integer inputs, power-of-two scales).
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -372,3 +374,22 @@ def test_nan_rows_follow_torch(tdt, dt):
         qn, sn = oq.quantized_tensor_rows(w.float().numpy(), dt, bits)
         assert np.array_equal(qt.numpy(), qn) and (qn[1] == 0).all()
         assert np.array_equal(st.float().numpy(), sn, equal_nan=True) and np.isnan(sn[1]).all()
+
+
+def test_codec_division_correction_exhaustive(tmp_path):
+    """The KV codec kernel replaces its per-element division by
+    x * RN(1/s) plus one residual FMA; tests/division_check.c verifies, for
+    every 16-bit x and scale in the codec's range (both formats), that this
+    rounds to the same 16-bit value as the true quotient, and that amax / 127
+    and amax / 7 come out bit-exact (compiled with gcc, all host threads)."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    src = os.path.join(os.path.dirname(os.path.abspath(__file__)), "division_check.c")
+    exe = str(tmp_path / "division_check")
+    subprocess.run([gcc, "-O2", "-fopenmp", "-ffp-contract=off", src, "-o", exe, "-lm"], check=True)
+    res = subprocess.run([exe], capture_output=True, text=True, timeout=600)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert " 0 mismatches" in res.stdout
