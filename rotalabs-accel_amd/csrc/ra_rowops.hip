@@ -309,19 +309,37 @@ __global__ __launch_bounds__(256) void quantize_rows_short_kernel(const uint16_t
     // holding inf) keeps the plain product x * (1 / sc): +-inf / NaN for
     // x / 0, 0 / NaN for x / inf, as the quotient.
     const float rinv = 1.0f / sc;
-    const bool correct = sc != 0.0f && __builtin_isfinite(sc);
     uint32_t lo = 0, hi = 0;
+    if (sc != 0.0f && __builtin_isfinite(sc)) {
+      // Finite, nonzero scale: every element is finite (a NaN or inf element
+      // makes amax, hence sc, NaN or inf), so the clamped integers plus 128
+      // lie in [0, 255]; convert and pack them four at a time, then flip the
+      // sign bits.
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float q0 = x[e] * rinv;
-      const float q1 = correct ? __builtin_fmaf(__builtin_fmaf(-q0, sc, x[e]), rinv, q0) : q0;
-      // (the rounded value goes through a register again: otherwise the
-      // compiler re-rounds the integral rint result to 16 bits)
-      const float r = rintf(fp32_rounded(A::rnd(fp32_rounded(q1))));
-      const int qi = r != r ? 0 : (int)__builtin_amdgcn_fmed3f(r, qlo, qhi);
-      const uint32_t b = (uint32_t)(uint8_t)(int8_t)qi;
-      if (e < 4) lo |= b << (8 * e);
-      else hi |= b << (8 * (e - 4));
+      for (int e = 0; e < 8; ++e) {
+        const float q0 = x[e] * rinv;
+        const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, sc, x[e]), rinv, q0);
+        // (the rounded value goes through a register again: otherwise the
+        // compiler re-rounds the integral rint result to 16 bits)
+        const float r = rintf(fp32_rounded(A::rnd(fp32_rounded(q1))));
+        const float b = __builtin_amdgcn_fmed3f(r, qlo, qhi) + 128.0f;
+        if (e < 4) lo = __builtin_amdgcn_cvt_pk_u8_f32(b, e, lo);
+        else hi = __builtin_amdgcn_cvt_pk_u8_f32(b, e - 4, hi);
+      }
+      lo ^= 0x80808080u;
+      hi ^= 0x80808080u;
+    } else {
+      // Zero scale (fp16 rounds the 1e-8 floor to 0), infinite or NaN: the
+      // plain product x * (1 / sc) is the quotient's +-inf / NaN / 0; NaN
+      // converts to 0.
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float r = rintf(A::rnd(fp32_rounded(x[e] * rinv)));
+        const int qi = r != r ? 0 : (int)__builtin_amdgcn_fmed3f(r, qlo, qhi);
+        const uint32_t b = (uint32_t)(uint8_t)(int8_t)qi;
+        if (e < 4) lo |= b << (8 * e);
+        else hi |= b << (8 * (e - 4));
+      }
     }
     store8(q + row * ldq + 8 * c, lo, hi);
     if (c == 0) scale[row] = A::out(sc);
