@@ -188,6 +188,151 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t *__restri
   }
 }
 
+// M = 1 with x staged once per workgroup in LDS: the four waves of a
+// workgroup copy x[0:K] into LDS with direct-to-LDS loads (issued before
+// their first weight loads), wait for those copies only, meet at a barrier,
+// and read their activation chunks from LDS. The L2 line requests of x --
+// as many per wave as its weight requests at two rows per wave, and charged
+// to the same per-CU budget of outstanding lines -- drop fourfold. The weight
+// streaming, the per-wave rows and the epilogue are those of
+// gemv_rows_kernel.
+constexpr int kRowsLdsMaxK = 16384;  // at most 32 KB of LDS per workgroup (2K bytes, dynamic)
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+template <int DT, int RW, bool GU>
+__global__ __launch_bounds__(256) void gemv_rows_lds_kernel(const uint16_t *__restrict__ x,
+                                                            const int8_t *w, int64_t ldw,  // (not restrict: the
+                                                            // first loads must stay in front of the copy wait)
+                                                            const float *__restrict__ scale,
+                                                            const void *__restrict__ bias, int bias_dt,
+                                                            uint16_t *__restrict__ y, int N, int K) {
+  using A = Act<DT>;
+  constexpr int NR = GU ? 2 * RW : RW;
+  constexpr int WLOADS = kRowsCh * NR;  // weight loads of the first step
+  extern __shared__ __attribute__((aligned(16))) uint16_t xl[];  // K elements
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = (blockIdx.x * 4 + wid) * RW;
+  // Waves past N (last workgroup only) copy, meet the barrier and compute on
+  // clamped rows like the others, and store nothing.
+  const int8_t *wr[NR];
+#pragma unroll
+  for (int t = 0; t < NR; ++t) {
+    const int n = min(n0 + t % RW, N - 1);
+    wr[t] = w + (int64_t)(t < RW ? n : N + n) * ldw + 16 * lane;
+  }
+  // Epilogue operands first (older than the copies, so the copy wait covers them).
+  float sc[RW], su[RW];
+  uint32_t bb[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int n = min(n0 + r, N - 1);
+    sc[r] = scale[n];
+    su[r] = GU ? scale[N + n] : 0.f;
+    bb[r] = 0;
+    if (!GU && bias) {
+      if (bias_dt == RA_F32) bb[r] = static_cast<const uint32_t *>(bias)[n];
+      else bb[r] = static_cast<const uint16_t *>(bias)[n];
+    }
+  }
+  // x -> LDS: 1 KB chunks, chunk j by wave j % 4, lane -> bytes 16 lane of
+  // the chunk (M0 = the chunk's LDS address; the copy writes M0 + 16 lane).
+  const int xbytes = 2 * K;  // K % 16 == 0: whole 16-byte pieces
+  const uint32_t lds0 = lds_addr(xl);
+  for (int j = wid; 1024 * j < xbytes; j += 4) {
+    const int off = 1024 * j + 16 * lane;
+    if (off < xbytes)
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds0 + 1024 * j),
+                   "v"(reinterpret_cast<const char *>(x) + off)
+                   : "memory", "m0");
+  }
+  float acc[NR];
+#pragma unroll
+  for (int t = 0; t < NR; ++t) acc[t] = 0.f;
+  // First step's weights (K >= 1024 * kRowsCh is required by the host; rows
+  // of inactive waves are clamped to N - 1: in bounds, never used).
+  const int full = K / (1024 * kRowsCh);  // whole steps of kRowsCh windows, >= 1
+  uint4 wv[kRowsCh][NR];
+#pragma unroll
+  for (int c = 0; c < kRowsCh; ++c)
+#pragma unroll
+    for (int t = 0; t < NR; ++t) wv[c][t] = *reinterpret_cast<const uint4 *>(wr[t] + 1024 * c);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WLOADS) : "memory");  // this wave's copies have landed
+  asm volatile("s_barrier" ::: "memory");                         // every wave's copies have landed
+
+  const uint16_t *xr = xl + 16 * lane;
+  for (int step = 0; step < full; ++step) {
+    const int k0 = 1024 * kRowsCh * step;
+    if (step > 0) {
+#pragma unroll
+      for (int c = 0; c < kRowsCh; ++c)
+#pragma unroll
+        for (int t = 0; t < NR; ++t) wv[c][t] = *reinterpret_cast<const uint4 *>(wr[t] + k0 + 1024 * c);
+    }
+    uint4 xa[kRowsCh], xb[kRowsCh];
+#pragma unroll
+    for (int c = 0; c < kRowsCh; ++c) {
+      xa[c] = *reinterpret_cast<const uint4 *>(xr + k0 + 1024 * c);
+      xb[c] = *reinterpret_cast<const uint4 *>(xr + k0 + 1024 * c + 8);
+    }
+    if (step == 0) {
+      // The first step's weights (loaded before the barrier) become opaque
+      // here: otherwise the compiler starts their dequantisation, and waits
+      // for them, in front of the barrier.
+#pragma unroll
+      for (int c = 0; c < kRowsCh; ++c)
+#pragma unroll
+        for (int t = 0; t < NR; ++t) {
+          uint32_t a0 = wv[c][t].x, a1 = wv[c][t].y, a2 = wv[c][t].z, a3 = wv[c][t].w;
+          asm volatile("" : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3)::"memory");
+          wv[c][t] = make_uint4(a0, a1, a2, a3);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < kRowsCh; ++c)
+#pragma unroll
+      for (int t = 0; t < NR; ++t) acc[t] = dot16<DT>(wv[c][t], xa[c], xb[c], acc[t]);
+  }
+  // Tail windows: lanes past K read the row's first 16 weights and x[0..15]
+  // (in bounds) and contribute zeros.
+  for (int k0 = 1024 * kRowsCh * full; k0 < K; k0 += 1024) {
+    const bool ok = k0 + 16 * lane + 16 <= K;
+    const int k = ok ? k0 : -16 * lane;
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    uint4 wt[NR];
+#pragma unroll
+    for (int t = 0; t < NR; ++t) {
+      wt[t] = *reinterpret_cast<const uint4 *>(wr[t] + k);
+      if (!ok) wt[t] = z;
+    }
+    uint4 xa = *reinterpret_cast<const uint4 *>(xr + k);
+    uint4 xb = *reinterpret_cast<const uint4 *>(xr + k + 8);
+    if (!ok) xa = xb = z;
+#pragma unroll
+    for (int t = 0; t < NR; ++t) acc[t] = dot16<DT>(wt[t], xa, xb, acc[t]);
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const float s0 = wave_sum_dpp(acc[r]);
+    const float s1 = GU ? wave_sum_dpp(acc[NR - RW + r]) : 0.f;
+    const int n = n0 + r;
+    if (lane == r && n < N) {
+      if (GU) {
+        y[n] = swiglu_out<A>(s0 * sc[r], s1 * su[r]);
+      } else {
+        float v = s0 * sc[r];
+        if (bias)
+          v += bias_dt == RA_F32 ? __uint_as_float(bb[r])
+                                 : (bias_dt == RA_F16 ? f16_to_f32((uint16_t)bb[r]) : bf16_to_f32((uint16_t)bb[r]));
+        y[n] = A::out(v);
+      }
+    }
+  }
+}
+
 // Short-K variant (K <= 4096, one step): a wave handles RP consecutive rows
 // one after another, loading row r+1 while it reduces row r, so the wave's
 // 4 KB of weight loads stay in flight during the dot products; x[0:M, 0:K] is
@@ -341,8 +486,31 @@ static void rows_go(const RowsParams &p, hipStream_t s) {
                      p.ldx, p.w, p.ldw, p.scale, p.bias, p.bias_dt, p.y, p.ldy, p.M, p.N, p.K);
 }
 
+template <int DT, int RW, bool GU>
+static void rows_lds_go(const RowsParams &p, hipStream_t s) {
+  const int64_t waves = ((int64_t)p.N + RW - 1) / RW;
+  hipLaunchKernelGGL((gemv_rows_lds_kernel<DT, RW, GU>), dim3((unsigned)((waves + 3) / 4)), dim3(256),
+                     (size_t)2 * p.K, s, p.x, p.w, p.ldw, p.scale, p.bias, p.bias_dt, p.y, p.N, p.K);
+}
+
 template <int DT, int MR, bool GU>
 static void rows_go_rw(const RowsParams &p, int rw, hipStream_t s) {
+  if constexpr (MR == 1) {
+    // x in LDS when it fits (one copy per workgroup instead of per wave) and
+    // the first step is whole
+    bool lds = p.K <= kRowsLdsMaxK && p.K >= 1024 * kRowsCh;
+#ifdef RA_TUNING
+    extern int g_rows_lds;  // 0 auto, -1 off
+    if (g_rows_lds == -1) lds = false;
+#endif
+    if (lds) {
+      if constexpr (!GU) {
+        if (rw == 4) return rows_lds_go<DT, 4, GU>(p, s);
+      }
+      if (rw >= 2) return rows_lds_go<DT, 2, GU>(p, s);
+      return rows_lds_go<DT, 1, GU>(p, s);
+    }
+  }
   if constexpr (MR == 1 && !GU) {
     if (rw == 4) return rows_go<DT, MR, 4, GU>(p, s);
   }
