@@ -194,7 +194,7 @@ def cpu_baseline(M, K, N, seed, budget_s):
 VARIANT_NAMES = {1: "skinny", 2: "tiled", 3: "generic", 4: "gemv", 5: "rows", 6: "batch"}
 # Kernel (symbol prefix in rocprofv3 traces) that each variant launches.
 VARIANT_KERNELS = {1: "skinny_kernel", 2: "tiled_dma_kernel", 3: "generic_kernel", 4: "gemv_kernel",
-                   5: "gemv_rows_kernel", 6: "batch_kernel"}
+                   5: "gemv_rows_lds_kernel", 6: "batch_kernel"}
 
 
 def run_decode(args, dev):

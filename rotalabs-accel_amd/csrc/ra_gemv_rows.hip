@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t *__restri
 // to the same per-CU budget of outstanding lines -- drop fourfold. The weight
 // streaming, the per-wave rows and the epilogue are those of
 // gemv_rows_kernel.
-constexpr int kRowsLdsMaxK = 16384;  // at most 32 KB of LDS per workgroup (2K bytes, dynamic)
+constexpr int kRowsLdsMaxK = 32768;  // at most 64 KB of LDS per workgroup (2K bytes, dynamic)
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
