@@ -504,10 +504,18 @@ static void rows_go_rw(const RowsParams &p, int rw, hipStream_t s) {
     if (g_rows_lds == -1) lds = false;
 #endif
     if (lds) {
+      // With x in LDS one row per wave streams fastest up to K = 16384
+      // (K=4096 N=11008: 9.2 us vs 9.7 with two rows, 10.2 with four); longer
+      // rows keep the count above.
+      int r = p.K <= 16384 ? 1 : rw;
+#ifdef RA_TUNING
+      extern int g_rows_rw;
+      if (g_rows_rw > 0) r = rw;
+#endif
       if constexpr (!GU) {
-        if (rw == 4) return rows_lds_go<DT, 4, GU>(p, s);
+        if (r == 4) return rows_lds_go<DT, 4, GU>(p, s);
       }
-      if (rw >= 2) return rows_lds_go<DT, 2, GU>(p, s);
+      if (r >= 2) return rows_lds_go<DT, 2, GU>(p, s);
       return rows_lds_go<DT, 1, GU>(p, s);
     }
   }
