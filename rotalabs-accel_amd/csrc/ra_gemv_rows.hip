@@ -202,8 +202,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
 
-template <int DT, int RW, bool GU>
-__global__ __launch_bounds__(256) void gemv_rows_lds_kernel(const uint16_t *__restrict__ x,
+template <int DT, int RW, bool GU, int WPG>
+__global__ __launch_bounds__(64 * WPG) void gemv_rows_lds_kernel(const uint16_t *__restrict__ x,
                                                             const int8_t *w, int64_t ldw,  // (not restrict: the
                                                             // first loads must stay in front of the copy wait)
                                                             const float *__restrict__ scale,
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(256) void gemv_rows_lds_kernel(const uint16_t *__re
   extern __shared__ __attribute__((aligned(16))) uint16_t xl[];  // K elements
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n0 = (blockIdx.x * 4 + wid) * RW;
+  const int n0 = (blockIdx.x * WPG + wid) * RW;
   // Waves past N (last workgroup only) copy, meet the barrier and compute on
   // clamped rows like the others, and store nothing.
   const int8_t *wr[NR];
@@ -238,11 +238,11 @@ __global__ __launch_bounds__(256) void gemv_rows_lds_kernel(const uint16_t *__re
       else bb[r] = static_cast<const uint16_t *>(bias)[n];
     }
   }
-  // x -> LDS: 1 KB chunks, chunk j by wave j % 4, lane -> bytes 16 lane of
+  // x -> LDS: 1 KB chunks, chunk j by wave j % WPG, lane -> bytes 16 lane of
   // the chunk (M0 = the chunk's LDS address; the copy writes M0 + 16 lane).
   const int xbytes = 2 * K;  // K % 16 == 0: whole 16-byte pieces
   const uint32_t lds0 = lds_addr(xl);
-  for (int j = wid; 1024 * j < xbytes; j += 4) {
+  for (int j = wid; 1024 * j < xbytes; j += WPG) {
     const int off = 1024 * j + 16 * lane;
     if (off < xbytes)
       asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds0 + 1024 * j),
@@ -489,8 +489,19 @@ static void rows_go(const RowsParams &p, hipStream_t s) {
 template <int DT, int RW, bool GU>
 static void rows_lds_go(const RowsParams &p, hipStream_t s) {
   const int64_t waves = ((int64_t)p.N + RW - 1) / RW;
-  hipLaunchKernelGGL((gemv_rows_lds_kernel<DT, RW, GU>), dim3((unsigned)((waves + 3) / 4)), dim3(256),
-                     (size_t)2 * p.K, s, p.x, p.w, p.ldw, p.scale, p.bias, p.bias_dt, p.y, p.N, p.K);
+  int wpg = 4;  // waves per workgroup (sharing one copy of x)
+#ifdef RA_TUNING
+  extern int g_rows_lds;  // > 0: waves per workgroup
+  if (g_rows_lds == 8 || g_rows_lds == 16) wpg = g_rows_lds;
+#endif
+#define RA_LDS_GO(WPG_)                                                                                       \
+  hipLaunchKernelGGL((gemv_rows_lds_kernel<DT, RW, GU, WPG_>), dim3((unsigned)((waves + WPG_ - 1) / WPG_)),  \
+                     dim3(64 * WPG_), (size_t)2 * p.K, s, p.x, p.w, p.ldw, p.scale, p.bias, p.bias_dt, p.y, p.N, \
+                     p.K)
+  if (wpg == 16) RA_LDS_GO(16);
+  else if (wpg == 8) RA_LDS_GO(8);
+  else RA_LDS_GO(4);
+#undef RA_LDS_GO
 }
 
 template <int DT, int MR, bool GU>
