@@ -98,7 +98,7 @@ __global__ __launch_bounds__(NW * 64) void batch_kernel(const uint16_t *__restri
     const int k_ = kb + KS * (st_);                                                                 \
     const int slot_ = (SLOT_);                                                                      \
     _Pragma("unroll") for (int j_ = 0; j_ < WL; ++j_) wreg[slot_][j_] =                             \
-        *reinterpret_cast<const uint4 *>(wsrc[j_] + k_);                                            \
+        load_stream16(wsrc[j_] + k_);                                                               \
     _Pragma("unroll") for (int s_ = 0; s_ < 4; ++s_)                                                \
         _Pragma("unroll") for (int mt_ = 0; mt_ < MT; ++mt_) xf[slot_][s_][mt_] =                   \
             *reinterpret_cast<const uint4 *>(xp[mt_] + k_ + 32 * s_);                               \

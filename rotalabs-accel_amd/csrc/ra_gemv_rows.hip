@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t *__restri
 #pragma unroll
     for (int c = 0; c < kRowsCh; ++c)
 #pragma unroll
-      for (int t = 0; t < NR; ++t) wv[c][t] = *reinterpret_cast<const uint4 *>(wr[t] + k0 + 1024 * c);
+      for (int t = 0; t < NR; ++t) wv[c][t] = load_stream16(wr[t] + k0 + 1024 * c);
 #pragma unroll
     for (int c = 0; c < kRowsCh; ++c)
 #pragma unroll
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t *__restri
     uint4 wv[NR], xa[MR], xb[MR];
 #pragma unroll
     for (int t = 0; t < NR; ++t) {
-      wv[t] = *reinterpret_cast<const uint4 *>(wr[t] + k);
+      wv[t] = load_stream16(wr[t] + k);
       if (!ok) wv[t] = z;
     }
 #pragma unroll
@@ -259,7 +259,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rows_lds_kernel(const uint16_t 
 #pragma unroll
   for (int c = 0; c < kRowsCh; ++c)
 #pragma unroll
-    for (int t = 0; t < NR; ++t) wv[c][t] = *reinterpret_cast<const uint4 *>(wr[t] + 1024 * c);
+    for (int t = 0; t < NR; ++t) wv[c][t] = load_stream16(wr[t] + 1024 * c);
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WLOADS) : "memory");  // this wave's copies have landed
   asm volatile("s_barrier" ::: "memory");                         // every wave's copies have landed
 
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rows_lds_kernel(const uint16_t 
 #pragma unroll
       for (int c = 0; c < kRowsCh; ++c)
 #pragma unroll
-        for (int t = 0; t < NR; ++t) wv[c][t] = *reinterpret_cast<const uint4 *>(wr[t] + k0 + 1024 * c);
+        for (int t = 0; t < NR; ++t) wv[c][t] = load_stream16(wr[t] + k0 + 1024 * c);
     }
     uint4 xa[kRowsCh], xb[kRowsCh];
 #pragma unroll
@@ -305,7 +305,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rows_lds_kernel(const uint16_t 
     uint4 wt[NR];
 #pragma unroll
     for (int t = 0; t < NR; ++t) {
-      wt[t] = *reinterpret_cast<const uint4 *>(wr[t] + k);
+      wt[t] = load_stream16(wr[t] + k);
       if (!ok) wt[t] = z;
     }
     uint4 xa = *reinterpret_cast<const uint4 *>(xr + k);
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(256) void gemv_rows_pipe_kernel(const uint16_t *__r
     for (int t = 0; t < NT; ++t) {
       const int8_t *row = w + (int64_t)(t ? N + n : n) * ldw;
 #pragma unroll
-      for (int c = 0; c < kRowsCh; ++c) dst[c][t] = *reinterpret_cast<const uint4 *>(row + off[c]);
+      for (int c = 0; c < kRowsCh; ++c) dst[c][t] = load_stream16(row + off[c]);
     }
   };
   load_row(0, wv[0]);

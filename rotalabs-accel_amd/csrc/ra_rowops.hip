@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void quantize_rows_short_kernel(const uint16_t
   for (int u = 0; u < U; ++u) {
     int64_t rr = row0 + (int64_t)u * RPW;
     rr = rr < rows ? rr : rows - 1;
-    v[u] = *reinterpret_cast<const uint4 *>(t + rr * ldt + 8 * cc);
+    v[u] = load_stream16(t + rr * ldt + 8 * cc);  // read once: non-temporal (72 -> 66 us on 256 MiB)
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
