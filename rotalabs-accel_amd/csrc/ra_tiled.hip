@@ -601,6 +601,8 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
   uint16_t *const yw = y + (int64_t)(m0 + wm * WM) * ldy + col_w;
   const uint32_t ldy32 = (uint32_t)ldy;
   const uint32_t lane_off = 4u * (uint32_t)g * ldy32 + (uint32_t)l32;
+  // Non-temporal stores: the tile is written once and not read back by this
+  // launch (M=2048 K=4096 N=11008: 153.3 -> 152.4 us, same-box A/B).
   auto store_blocks = [&](auto guard_c, auto bias_c) {
     constexpr bool GUARD = decltype(guard_c)::value, HAS_BIAS = decltype(bias_c)::value;
     if constexpr (GU) {
@@ -615,8 +617,8 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
           for (int e = 0; e < 16; ++e) {
             const int r = bi * 32 + (e & 3) + 8 * (e >> 2);
             if (!GUARD || r < rows_left)
-              yw[lane_off + (uint32_t)r * ldy32 + 32u * bj] =
-                  swiglu_out<Ac>(acc[bi][bj][e] * sg, acc[bi][bj + BNB / 2][e] * su);
+              __builtin_nontemporal_store((uint16_t)swiglu_out<Ac>(acc[bi][bj][e] * sg, acc[bi][bj + BNB / 2][e] * su),
+                                          &yw[lane_off + (uint32_t)r * ldy32 + 32u * bj]);
           }
       }
     } else {
@@ -634,7 +636,7 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
             if (!GUARD || r < rows_left) {
               float v = acc[bi][bj][e] * sn;
               if (HAS_BIAS) v += bn;
-              yw[lane_off + (uint32_t)r * ldy32 + 32u * bj] = Ac::out(v);
+              __builtin_nontemporal_store((uint16_t)Ac::out(v), &yw[lane_off + (uint32_t)r * ldy32 + 32u * bj]);
             }
           }
       }
