@@ -51,7 +51,12 @@ __global__ __launch_bounds__(NW * 64) void batch_kernel(const uint16_t *__restri
   const int n0 = blockIdx.x * (16 * RT);
   const int m0 = blockIdx.y * (16 * MT);
 
-  __shared__ __attribute__((aligned(16))) uint8_t tbuf[NW][WROWS * KS];
+  // LDS: the waves' transposition slots during the K loop, then their
+  // partial sums for the split-K combine.
+  constexpr int NACC = NTW * MT;
+  constexpr int SLOT_BYTES = NW * WROWS * KS;
+  constexpr int RED_BYTES = NW > 1 ? NW * NACC * 64 * 16 : 16;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SLOT_BYTES > RED_BYTES ? SLOT_BYTES : RED_BYTES];
 
   // Stage loads: load j covers wave rows 8j .. 8j+7; lane -> row 8j + lane/8,
   // 16-byte chunk lane%8 of the row's 128-byte stage segment. Rows past N are
@@ -77,7 +82,7 @@ __global__ __launch_bounds__(NW * 64) void batch_kernel(const uint16_t *__restri
     const int m = m0 + 16 * mt + r;
     xp[mt] = x + (int64_t)(m < M ? m : 0) * ldx + 8 * g;
   }
-  uint8_t *const slot = tbuf[wid];
+  uint8_t *const slot = smem + wid * (WROWS * KS);
 
   const int kb = wid * kslice;
   const int ke = min(K, kb + kslice);
@@ -144,10 +149,10 @@ __global__ __launch_bounds__(NW * 64) void batch_kernel(const uint16_t *__restri
 
   // Combine the NW split-K partial sums in a fixed order, then the epilogue.
   // Output tile i = t*MT + mt (t < RT) is finished by wave i % NW.
-  constexpr int NACC = NTW * MT;
   constexpr int NOUT = RT * MT;
-  __shared__ f32x4 red[NW > 1 ? NW : 1][NACC][64];
+  f32x4(*red)[NACC][64] = reinterpret_cast<f32x4(*)[NACC][64]>(smem);
   if (NW > 1) {
+    __syncthreads();  // every wave is done with its transposition slot
 #pragma unroll
     for (int t = 0; t < NTW; ++t)
 #pragma unroll
@@ -205,7 +210,10 @@ bool gateup_batch_supported(const GateUpArgs &a) {
 template <int DT, int MT, int RT, int NW, bool GU>
 static void batch_go(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale, const void *bias,
                      int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t s) {
-  constexpr int D = MT == 1 ? 4 : (MT == 2 ? 3 : 2);  // stages in flight (registers: D * (8 + 16 MT) per lane)
+  // stages in flight per wave (registers: D * (8 + 16 MT) per lane); halved
+  // with 8 or more waves per workgroup (two or more waves per SIMD)
+  constexpr int D4 = MT == 1 ? 4 : (MT == 2 ? 3 : 2);
+  constexpr int D = NW >= 8 ? (D4 > 2 ? D4 / 2 : 1) : D4;
   const int kslice = (int)(((K + NW - 1) / NW + batch::KS - 1) / batch::KS * batch::KS);
   const dim3 grid((unsigned)((N + 16 * RT - 1) / (16 * RT)), (unsigned)((M + 16 * MT - 1) / (16 * MT)));
   hipLaunchKernelGGL((batch_kernel<DT, MT, RT, NW, D, GU>), grid, dim3(NW * 64), 0, s,
@@ -215,13 +223,49 @@ static void batch_go(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, c
 
 // M tiles per workgroup: one 16-row activation tile up to M = 16, then the
 // whole batch in one workgroup (activations re-read once per weight tile).
+// LDS bytes of batch_kernel<., MT, RT, NW, ., GU> (the larger of the
+// transposition slots and the split-K partial sums).
+template <int MT, int RT, int NW, bool GU>
+constexpr int batch_lds_bytes() {
+  constexpr int ntw = GU ? 2 * RT : RT;
+  constexpr int slots = NW * 16 * ntw * batch::KS, red = NW * ntw * MT * 64 * 16;
+  return slots > red ? slots : red;
+}
+
+template <int DT, int MT, int RT, int NW, bool GU>
+static void batch_go_nw(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale, const void *bias,
+                        int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t s) {
+  if constexpr (batch_lds_bytes<MT, RT, NW, GU>() <= 160 * 1024)
+    batch_go<DT, MT, RT, NW, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  else
+    batch_go<DT, MT, RT, 4, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+}
+
+template <int DT, int RT, int NW, bool GU>
+static void batch_dispatch_mt(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
+                              const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                              hipStream_t s) {
+  if (M <= 16) batch_go_nw<DT, 1, RT, NW, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  else if (M <= 32) batch_go_nw<DT, 2, RT, NW, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  else batch_go_nw<DT, 4, RT, NW, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+}
+
 template <int DT, int RT, bool GU>
 static void batch_dispatch_rt(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
                               const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                               hipStream_t s) {
-  if (M <= 16) batch_go<DT, 1, RT, 4, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
-  else if (M <= 32) batch_go<DT, 2, RT, 4, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
-  else batch_go<DT, 4, RT, 4, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+#ifdef RA_TUNING
+  extern int g_batch_nw;
+  if (g_batch_nw == 4) return batch_dispatch_mt<DT, RT, 4, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  if (g_batch_nw == 16) return batch_dispatch_mt<DT, RT, 16, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+#endif
+  // Eight waves (each half of the K slice of four, two waves per SIMD, half
+  // the stages in flight) measured faster for RT >= 2 (M=4 K=4096 N=11008
+  // 12.6 -> 11.4 us, M=17 K=8192 N=57344 106 -> 88) and mixed for RT = 1.
+  if constexpr (RT >= 2)
+    batch_dispatch_mt<DT, RT, 8, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  else
+    batch_dispatch_mt<DT, RT, 4, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
 }
 
 static int device_cus() {

@@ -97,6 +97,23 @@ def test_exact_known_answer_all_variants(gpu, M, K, N, dt):
     assert ran == sum(not _may_refuse(v, M, K) for v in ALL_VARIANTS)
 
 
+# Wide N: the small-batch kernel takes 32 or 48 weight rows per workgroup
+# (RT = 2, 3) and splits K over 8 waves, K slices of 128 to 640; K = 1152
+# leaves three of the eight waves without a slice, K = 128 all but one.
+WIDE_BATCH_SHAPES = [(4, 1152, 11008), (16, 128, 8000), (33, 4096, 11008), (64, 1024, 6000), (20, 640, 9000)]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K,N", WIDE_BATCH_SHAPES)
+def test_exact_known_answer_wide_batch(gpu, M, K, N, dt):
+    x, q, s, b, exact = _exact_case(M, K, N, dt, seed=M + K + N, dev=gpu, bias=(K % 256 == 128))
+    print(f"  wide batch M={M} K={K} N={N} {dt}", flush=True)
+    want = exact.to(dt)
+    for v in (_backend.VARIANT_AUTO, BATCH):
+        y = _run(x, q, s, b, v).cpu()
+        assert torch.equal(y, want), f"variant {v}: {(y.double() - exact).abs().max()}"
+
+
 def test_exact_fp32_activations(gpu):
     x, q, s, b, exact = _exact_case(9, 200, 70, torch.float32, seed=5, dev=gpu, bias=True)
     y = _run(x, q, s, b).cpu()
