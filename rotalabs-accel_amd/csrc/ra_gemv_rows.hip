@@ -138,29 +138,35 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t *__restri
 #pragma unroll
         for (int m = 0; m < MR; ++m) acc[t][m] = dot16<DT>(wv[c][t], xa[c][m], xb[c][m], acc[t][m]);
   }
-  // Tail: single windows; K % 16 == 0, so a lane's 16-byte chunk is all in or
-  // all out. Lanes past K re-read the first 16 elements of their rows
-  // (offset -16*lane from their own column; K >= 16) and contribute zeros.
-  for (; k0 < K; k0 += 1024) {
-    const bool ok = k0 + 16 * lane + 16 <= K;
-    const int k = ok ? k0 : -16 * lane;
+  // Tail (fewer than kRowsCh windows left): one step of kRowsCh windows whose
+  // loads are all issued before the first use, as in the main loop. K % 16
+  // == 0, so a lane's 16-byte chunk is all in or all out; chunks past K
+  // re-read the first 16 elements of their rows (offset -16*lane from the
+  // lane's own column; K >= 16) and contribute zeros.
+  if (k0 < K) {
+    uint4 wv[kRowsCh][NR], xa[kRowsCh][MR], xb[kRowsCh][MR];
+    bool ok[kRowsCh];
+#pragma unroll
+    for (int c = 0; c < kRowsCh; ++c) {
+      ok[c] = k0 + 1024 * c + 16 * lane + 16 <= K;
+      const int k = ok[c] ? k0 + 1024 * c : -16 * lane;
+#pragma unroll
+      for (int t = 0; t < NR; ++t) wv[c][t] = load_stream16(wr[t] + k);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        xa[c][m] = *reinterpret_cast<const uint4 *>(xr[m] + k);
+        xb[c][m] = *reinterpret_cast<const uint4 *>(xr[m] + k + 8);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the step is issued before the first wait
     const uint4 z = make_uint4(0, 0, 0, 0);
-    uint4 wv[NR], xa[MR], xb[MR];
 #pragma unroll
-    for (int t = 0; t < NR; ++t) {
-      wv[t] = load_stream16(wr[t] + k);
-      if (!ok) wv[t] = z;
-    }
+    for (int c = 0; c < kRowsCh; ++c)
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      xa[m] = *reinterpret_cast<const uint4 *>(xr[m] + k);
-      xb[m] = *reinterpret_cast<const uint4 *>(xr[m] + k + 8);
-      if (!ok) xa[m] = xb[m] = z;
-    }
+      for (int t = 0; t < NR; ++t)
 #pragma unroll
-    for (int t = 0; t < NR; ++t)
-#pragma unroll
-      for (int m = 0; m < MR; ++m) acc[t][m] = dot16<DT>(wv[t], xa[m], xb[m], acc[t][m]);
+        for (int m = 0; m < MR; ++m)
+          acc[t][m] = dot16<DT>(ok[c] ? wv[c][t] : z, ok[c] ? xa[c][m] : z, ok[c] ? xb[c][m] : z, acc[t][m]);
   }
 
   // Reduce over the wave (DPP); lane r stores row n0 + r. Same arithmetic as
@@ -296,23 +302,29 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rows_lds_kernel(const uint16_t 
 #pragma unroll
       for (int t = 0; t < NR; ++t) acc[t] = dot16<DT>(wv[c][t], xa[c], xb[c], acc[t]);
   }
-  // Tail windows: lanes past K read the row's first 16 weights and x[0..15]
-  // (in bounds) and contribute zeros.
-  for (int k0 = 1024 * kRowsCh * full; k0 < K; k0 += 1024) {
-    const bool ok = k0 + 16 * lane + 16 <= K;
-    const int k = ok ? k0 : -16 * lane;
-    const uint4 z = make_uint4(0, 0, 0, 0);
-    uint4 wt[NR];
+  // Tail (fewer than kRowsCh windows left): one step with all its weight
+  // loads issued before the first use; chunks past K read the row's first
+  // 16 weights and x[0..15] (in bounds) and contribute zeros.
+  const int kt = 1024 * kRowsCh * full;
+  if (kt < K) {
+    uint4 wt[kRowsCh][NR];
+    bool ok[kRowsCh];
+    int kk[kRowsCh];
 #pragma unroll
-    for (int t = 0; t < NR; ++t) {
-      wt[t] = load_stream16(wr[t] + k);
-      if (!ok) wt[t] = z;
+    for (int c = 0; c < kRowsCh; ++c) {
+      ok[c] = kt + 1024 * c + 16 * lane + 16 <= K;
+      kk[c] = ok[c] ? kt + 1024 * c : -16 * lane;
+#pragma unroll
+      for (int t = 0; t < NR; ++t) wt[c][t] = load_stream16(wr[t] + kk[c]);
     }
-    uint4 xa = *reinterpret_cast<const uint4 *>(xr + k);
-    uint4 xb = *reinterpret_cast<const uint4 *>(xr + k + 8);
-    if (!ok) xa = xb = z;
+    const uint4 z = make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int t = 0; t < NR; ++t) acc[t] = dot16<DT>(wt[t], xa, xb, acc[t]);
+    for (int c = 0; c < kRowsCh; ++c) {
+      const uint4 xa = *reinterpret_cast<const uint4 *>(xr + kk[c]);
+      const uint4 xb = *reinterpret_cast<const uint4 *>(xr + kk[c] + 8);
+#pragma unroll
+      for (int t = 0; t < NR; ++t) acc[t] = dot16<DT>(ok[c] ? wt[c][t] : z, ok[c] ? xa : z, ok[c] ? xb : z, acc[t]);
+    }
   }
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
