@@ -16,6 +16,9 @@ Metric: int8_gemm HBM GB/s at M=1 and TFLOP/s at M=2048 (K=4096, N=11008).
 * ``w8a8``: the opt-in W8A8 route (int8 activations, int8 MFMA) at the
   prefill shape, TOPS against the dense int8 peak (5033 TOP/s), beside
   hipBLASLt's int8 GEMM (torch._int_mm).
+* ``shapes``: the other decode shapes (M=1: K=4096 N=4096, K=11008 N=4096)
+  and the small-batch shapes (M=4, 16, 64 at K=4096 N=11008), GB/s per
+  call, timed like the headline.
 * ``mlp``: the fused decoder MLP block (RMSNorm -> int8 gate/up + SwiGLU ->
   int8 down, bf16, H=8192, I=28672) per call at M=1 (GB/s) and M=4096
   (TFLOP/s), graph replay.
@@ -56,7 +59,7 @@ def parse():
     p.add_argument("--prefill-steps", type=int, default=300)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", choices=("all", "decode", "prefill", "mlp", "w8a8"), default="all",
+    p.add_argument("--only", choices=("all", "decode", "prefill", "mlp", "w8a8", "shapes"), default="all",
                    help="run one workload only (for profiler runs)")
     p.add_argument("--no-mlp", action="store_true", help="skip the fused-MLP timing")
     p.add_argument("--no-graph", action="store_true",
@@ -323,6 +326,41 @@ def run_w8a8(args, dev):
 MLP = (8192, 28672)   # hidden, intermediate (70B-class decoder MLP, bf16)
 
 
+# The other decode (M=1) and small-batch shapes of the workload set, timed
+# like the headline (graph replay, weight copies cycled past the 256 MB
+# Infinity Cache): (group, M, K, N, seed).
+CONFIG_SHAPES = (("decode", 1, 4096, 4096, 1), ("decode", 1, 11008, 4096, 3),
+                 ("small_batch", 4, 4096, 11008, 4), ("small_batch", 16, 4096, 11008, 5),
+                 ("small_batch", 64, 4096, 11008, 6))
+
+
+def run_shapes(args, dev):
+    """Decode and small-batch shapes beside the headline: list of dicts."""
+    import torch
+    import rotalabs_accel as ra
+    from rotalabs_accel import _backend
+    from workloads import gemm_bytes, gemm_case
+    rows = []
+    for group, M, K, N, seed in CONFIG_SHAPES:
+        c = gemm_case(M, K, N, seed, device=dev, outlier_rows=M > 1)
+        ncop = max(2, -(-600_000_000 // (N * K)))
+        copies = [c.q] + [c.q.clone() for _ in range(ncop - 1)]
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        launcher = GemmLauncher(c.x, copies, c.s, y)
+        launcher.run(1)
+        torch.cuda.synchronize()
+        assert torch.equal(y, ra.int8_gemm(c.x, c.q, c.s)), "timed path differs from int8_gemm"
+        ms, _ = time_graph(launcher, 600, 60, per_graph=10 * ncop)
+        gbs = gemm_bytes(M, K, N) / (ms * 1e-3) / 1e9
+        variant = _backend.load().ra_w8a16_gemm_select(M, N, K, _backend.F16)
+        rec = {"group": group, "M": M, "K": K, "N": N, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+               "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "kernel_variant": VARIANT_NAMES.get(variant, str(variant))}
+        rows.append(rec)
+        log(f"{group} M={M} K={K} N={N}: {rec['us']} us, {rec['GB/s']} GB/s ({rec['frac_hbm']:.1%} of HBM peak)")
+        del copies, launcher, c, y
+    return rows
+
+
 def run_mlp(args, dev):
     """Fused decoder MLP block (RMSNorm -> gate/up + SwiGLU -> down, bf16,
     H=8192, I=28672) at M=1 and M=4096, random int8 weights generated on the
@@ -434,6 +472,9 @@ def main():
     w8a8 = None
     if args.only in ("all", "w8a8"):
         w8a8 = run_w8a8(args, dev)
+    shapes = None
+    if args.only in ("all", "shapes"):
+        shapes = run_shapes(args, dev)
     mlp = None
     if args.only == "mlp" or (args.only == "all" and not args.no_mlp):
         mlp = run_mlp(args, dev)
@@ -485,6 +526,10 @@ def main():
                                                      VARIANT_KERNELS.get(pvariant, ""))},
         },
     }
+    if shapes is not None:
+        out["shapes"] = {"workload": "the other decode (M=1) and small-batch shapes: fp16 x ~N(0,1) (1% of "
+                                     "rows x20 for M > 1), int8 per-channel W from N(0,0.02), weight copies "
+                                     "cycled past the Infinity Cache, HIP graph replay", "rows": shapes}
     if w8a8 is not None:
         out["w8a8"] = w8a8
     if mlp is not None:
