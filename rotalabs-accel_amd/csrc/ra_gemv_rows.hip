@@ -501,10 +501,13 @@ static void rows_go(const RowsParams &p, hipStream_t s) {
 template <int DT, int RW, bool GU>
 static void rows_lds_go(const RowsParams &p, hipStream_t s) {
   const int64_t waves = ((int64_t)p.N + RW - 1) / RW;
-  int wpg = 4;  // waves per workgroup (sharing one copy of x)
+  // Waves per workgroup (sharing one copy of x): 8 up to N = 8192 (K=14336
+  // N=4096 12.1 -> 11.4 us, K=28672 N=8192 37.2 -> 36.4), 4 above (K=4096
+  // N=11008 8.40 vs 8.54 with 8, K=8192 N=57344 65.3 vs 68.5).
+  int wpg = p.N <= 8192 ? 8 : 4;
 #ifdef RA_TUNING
   extern int g_rows_lds;  // > 0: waves per workgroup
-  if (g_rows_lds == 8 || g_rows_lds == 16) wpg = g_rows_lds;
+  if (g_rows_lds == 4 || g_rows_lds == 8 || g_rows_lds == 16) wpg = g_rows_lds;
 #endif
 #define RA_LDS_GO(WPG_)                                                                                       \
   hipLaunchKernelGGL((gemv_rows_lds_kernel<DT, RW, GU, WPG_>), dim3((unsigned)((waves + WPG_ - 1) / WPG_)),  \

@@ -71,6 +71,7 @@ def _exact_case(M, K, N, dt, seed, dev, bias=False):
 
 EXACT_SHAPES = [
     (1, 64, 16), (1, 48, 43), (2, 4096, 64), (2, 1008, 8202), (2, 2048, 4100), (1, 11008, 40), (3, 128, 77),
+    (1, 4096, 4101), (1, 5120, 37), (1, 16400, 300), (1, 6144, 11003),
     (16, 1040, 33),
     (17, 64, 130), (33, 96, 50), (64, 256, 96), (65, 256, 300), (256, 128, 128), (300, 320, 200),
     (513, 1024, 129), (1000, 64, 17),
