@@ -232,9 +232,11 @@ def _swiglu_chain64(g64, u64, dt):
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 # (5, 512, 8192) and (20, 256, 8192): the small-batch kernel with 32 gate/up
-# rows per workgroup and 8 waves (one and two 16-row activation tiles).
+# rows per workgroup and 8 waves (one and two 16-row activation tiles);
+# (1, 4096, 6000): the M=1 kernel with x in LDS, 8 waves per workgroup, the
+# last workgroup partly past I.
 @pytest.mark.parametrize("M,K,inter", [(1, 1024, 512), (5, 512, 300), (17, 2048, 640), (64, 256, 128),
-                                        (5, 512, 8192), (20, 256, 8192),
+                                        (5, 512, 8192), (20, 256, 8192), (1, 4096, 6000),
                                         (100, 512, 96), (300, 1024, 200), (320, 128, 8704), (450, 128, 11264)])
 def test_gateup_swiglu_vs_oracle(gpu, dt, M, K, inter):
     g = torch.Generator().manual_seed(M + K)
