@@ -28,8 +28,8 @@
 //    fp32 accumulators in the epilogue, one rounding to the output dtype.
 //  * XCD-aware tile order: hardware deals workgroups round-robin over the 8
 //    XCDs; workgroup b is remapped so each XCD owns a contiguous range of the
-//    grouped (8 M-tiles per group) tile order and its L2 keeps the shared
-//    weight columns and activation rows.
+//    grouped (8 M-tiles per group; 4 in the direct-to-LDS kernel) tile order
+//    and its L2 keeps the shared weight columns and activation rows.
 // GU (gate/up + SwiGLU): the 128 B rows of a tile are 64 gate rows and the
 // 64 matching up rows, arranged so that each wave's two 32-column blocks are
 // the gate and up values of the same 32 output columns.
@@ -337,13 +337,17 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
   constexpr int OUTN = GU ? BN / 2 : BN;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE];
 
-  // ---- tile coordinates (XCD-aware, grouped along M; as tiled_kernel) ----
+  // ---- tile coordinates (XCD-aware, grouped along M as in tiled_kernel) ----
   const int T = tiles_m * tiles_n;
   const int b = blockIdx.x;
   const int xcd = b & 7, idx = b >> 3;
   const int per = T >> 3, rem = T & 7;
   const int t = xcd * per + (xcd < rem ? xcd : rem) + idx;
-  constexpr int GM = 8;
+  // Groups of 4 M-tiles: an XCD's 32 concurrent tiles are 4 M-tiles x 8
+  // weight-column tiles, whose per-K-tile operands (4 x 256 fp16 rows, 8 x BN
+  // int8 rows) are fewer bytes than 8 x 4 (M=2048 K=4096 N=11008: 153.7 ->
+  // 152.4-153.4 us, same-box A/B).
+  constexpr int GM = 4;
   const int span = GM * tiles_n;
   const int first_m = (t / span) * GM;
   const int gm = min(tiles_m - first_m, GM);
