@@ -287,7 +287,7 @@ def run_w8a8(args, dev):
             for i in range(n):
                 if self.quant:
                     _backend.check(lib.ra_quantize_act_rows(cp.x.data_ptr(), Kp, _backend.F16, Mp, Kp,
-                                                            xq.data_ptr(), Kp, xs.data_ptr(), st))
+                                                            xq.data_ptr(), Kp, xs.data_ptr(), 127.0, st))
                 _backend.check(lib.ra_w8a8_gemm(xq.data_ptr(), Kp, xs.data_ptr(), wcopies[i % 3].data_ptr(), Kp,
                                                 cp.s.data_ptr(), None, 0, y.data_ptr(), Np, _backend.F16,
                                                 Mp, Np, Kp, st))

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define RA_ABI_VERSION 4
+#define RA_ABI_VERSION 5
 
 enum ra_dtype { RA_F16 = 0, RA_BF16 = 1, RA_F32 = 2 };
 
@@ -188,15 +188,18 @@ int ra_quantize_rows(const void *t, int64_t ldt, int t_dtype,
  * W8A8 route, step 1: per-row dynamic int8 quantisation of the activations
  * x[M,K] (fp16 or bf16), as _int8_gemm_cublas computes it
  * (src/rotalabs_accel/kernels/quantized_matmul.py:85-87), every op rounded to
- * x_dtype as torch does: a = max(max_k |x[m,k]|, 1e-5) (NaN propagates),
- * xs[m] = a / 127, mult = reciprocal(a) * 127 (torch's evaluation of 127 / a),
- * q[m,k] = clamp(round_half_even(x[m,k] * mult), -128, 127) (NaN -> 0).
+ * x_dtype as torch does on the CPU, with c = act_scale (the reference's
+ * default is 127) taken as an fp32 value: a = max(max_k |x[m,k]|, 1e-5) (NaN
+ * propagates), xs[m] = a / c (true division), mult = reciprocal(a) * c
+ * (torch's evaluation of c / a), q[m,k] = clamp(round_half_even(x[m,k] *
+ * mult), -128, 127) (NaN -> 0).
  * q: int8 [M, ldq]; xs: [M] in x_dtype. K = 0 is an error (as torch's
  * amax over an empty row is).
  */
 int ra_quantize_act_rows(const void *x, int64_t ldx, int x_dtype,
                          int64_t M, int64_t K,
-                         int8_t *q, int64_t ldq, void *xs, void *stream);
+                         int8_t *q, int64_t ldq, void *xs, float act_scale,
+                         void *stream);
 
 /*
  * W8A8 route, step 2: int8 x int8 GEMM on the int8 matrix cores,

@@ -48,6 +48,32 @@ def rmsnorm_ref(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Te
     return (xf * r).to(x.dtype) * w
 
 
+def rmsnorm_exact_ref(x32: np.ndarray, w32: np.ndarray, eps: float = 1e-6, dtype: str = "bf16",
+                      out_dtype: str | None = None) -> np.ndarray:
+    """normalization.py:43-45 with its fp32 ops exactly rounded.
+
+    The fallback computes ``mean(x.float()**2)`` as an fp32 reduction whose
+    last bit depends on the summation order (torch's CPU and GPU orders
+    differ). Here the fp32 squares (exact for 16-bit x) are summed in float64
+    and rounded once to fp32 -- the exactly rounded fp32 sum -- and the rest
+    are single IEEE fp32 ops as in the fallback:
+      s = fl32(sum_k fl32(x_k^2)); m = fl32(s / H); v = fl32(m + fl32(eps));
+      r = fl32(1 / fl32(sqrt(v))); h = round_x(fl32(x * r)); y = round_y(h * w)
+    x32, w32: values (as fp32) of 16-bit tensors of ``dtype`` (x) and
+    ``out_dtype`` (w, default the same); returns y's values as fp32.
+    """
+    from oracle.quant import round_to
+    out_dtype = out_dtype or dtype
+    x32 = np.asarray(x32, np.float32)
+    sq = (x32 * x32).astype(np.float32)
+    s = sq.astype(np.float64).sum(axis=-1, keepdims=True).astype(np.float32)
+    m = (s / np.float32(x32.shape[-1])).astype(np.float32)
+    v = (m + np.float32(eps)).astype(np.float32)
+    r = (np.float32(1) / np.sqrt(v)).astype(np.float32)
+    h = round_to((x32 * r).astype(np.float32), dtype)
+    return round_to((h * np.asarray(w32, np.float32)).astype(np.float32), out_dtype)
+
+
 def rmsnorm_residual_ref(x: torch.Tensor, r: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """normalization.py:48-64 on CPU tensors."""
     v = (x + r).float()

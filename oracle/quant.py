@@ -145,23 +145,25 @@ def quantized_tensor_rows(t32: np.ndarray, dtype: str = "f32", bits: int = 8):
 
 
 # ------------------------------------------------------------- W8A8 route
-def quantize_activations_rows(x32: np.ndarray, dtype: str = "f16"):
+def quantize_activations_rows(x32: np.ndarray, dtype: str = "f16", act_scale: float = 127.0):
     """Closed form of the activation quantisation of _int8_gemm_cublas
     (src/rotalabs_accel/kernels/quantized_matmul.py:85-87) over rows of
-    x (M, K), every op rounded to ``dtype`` as torch's tensor ops do:
+    x (M, K), every op rounded to ``dtype`` as torch's CPU tensor ops do,
+    with c = fp32(act_scale) (127 in the reference's default):
       a    = max(|x|.amax(1), round(1e-5))          (:85; NaN propagates)
-      xs   = round(a / 127)                         (:86)
-      mult = round(round(1 / a) * 127)              (:87; torch evaluates
-                                                     127 / a as reciprocal * 127)
+      xs   = round(a / c)                           (:86; true division)
+      mult = round(round(1 / a) * c)                (:87; torch evaluates
+                                                     c / a as reciprocal * c)
       q    = int8(clamp(rne(round(x * mult)), -128, 127)), NaN -> 0
     Returns (q int8 (M, K), xs fp32 values of ``dtype`` (M,))."""
     x32 = np.asarray(x32, dtype=np.float32)
+    c = np.float32(act_scale)
     with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
         a = np.abs(x32).max(axis=1)
         a = np.maximum(a, round_to(np.float32(1e-5).reshape(1), dtype)[0]).astype(np.float32)
-        xs = round_to((a / np.float32(127)).astype(np.float32), dtype)
+        xs = round_to((a / c).astype(np.float32), dtype)
         recip = round_to((np.float32(1) / a).astype(np.float32), dtype)
-        mult = round_to((recip * np.float32(127)).astype(np.float32), dtype)
+        mult = round_to((recip * c).astype(np.float32), dtype)
         r = np.rint(round_to((x32 * mult[:, None]).astype(np.float32), dtype))
     q = np.where(np.isnan(r), 0, np.clip(r, -128, 127)).astype(np.int8)
     return q, xs

@@ -225,12 +225,13 @@ int ra_quantize_rows(const void *t, int64_t ldt, int t_dtype, int64_t rows, int6
 }
 
 int ra_quantize_act_rows(const void *x, int64_t ldx, int x_dtype, int64_t M, int64_t K, int8_t *q, int64_t ldq,
-                         void *xs, void *stream) {
+                         void *xs, float act_scale, void *stream) {
   if (M < 0 || K < 0 || M > INT32_MAX || K > INT32_MAX) return RA_ERR_ARG;
   if (x_dtype != RA_F16 && x_dtype != RA_BF16) return RA_ERR_DTYPE;
   if (M == 0) return RA_OK;
   if (K == 0 || !x || !q || !xs || ldx < K || ldq < K) return RA_ERR_ARG;  // torch's amax rejects K = 0
-  return to_status(quantize_act_launch(x, ldx, x_dtype, M, K, q, ldq, xs, static_cast<hipStream_t>(stream)));
+  return to_status(
+      quantize_act_launch(x, ldx, x_dtype, M, K, q, ldq, xs, act_scale, static_cast<hipStream_t>(stream)));
 }
 
 int ra_w8a8_gemm(const int8_t *xq, int64_t ldxq, const void *xs, const int8_t *w, int64_t ldw, const float *scale,

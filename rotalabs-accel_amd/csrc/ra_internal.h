@@ -102,7 +102,7 @@ struct W8A8Args {
   int64_t M, N, K;
 };
 hipError_t quantize_act_launch(const void *x, int64_t ldx, int x_dt, int64_t M, int64_t K, int8_t *q, int64_t ldq,
-                               void *xs, hipStream_t s);
+                               void *xs, float act_scale, hipStream_t s);
 bool w8a8_tiled_supported(const W8A8Args &a);
 hipError_t w8a8_launch(const W8A8Args &a, hipStream_t s);
 

@@ -24,13 +24,31 @@ __device__ __forceinline__ float block_reduce(float v, float *smem) {
   return r;
 }
 
+// Workgroup sum of fp64 values (fixed order).
+__device__ __forceinline__ double block_sum_f64(double v, double *smem) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) smem[wid] = v;
+  __syncthreads();
+  double r = smem[0];
+#pragma unroll
+  for (int i = 1; i < kRowThreads / 64; ++i) r += smem[i];
+  return r;
+}
+
 // y = round_y( round_x(v * rsqrt(mean(v^2) + eps)) * w ) with v = x, as
 // rmsnorm_torch (src/rotalabs_accel/kernels/normalization.py:43-45): the
 // normalised value is stored in x's dtype, then multiplied by the weight in
 // the promoted dtype. With a residual r, v = round_s(x + r) in s, the
 // promotion of x's and r's dtypes, as rmsnorm_residual_torch (:60-62)
 // computes (x + residual) before .float().
-// rsqrt is 1/sqrt with both operations correctly rounded (no approximation).
+// The fp32 squares (exact for 16-bit v) are summed in fp64 and the sum is
+// rounded once to fp32: the exactly rounded fp32 sum, whatever the order
+// (the reference's fp32 reduction depends on its order; an order-dependent
+// last bit of the sum moves rsqrt by an ulp and can flip the 16-bit
+// rounding of an element of the row). mean = sum / hidden, + eps and
+// rsqrt = 1 / sqrt are fp32 operations, each correctly rounded.
 __global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(const void *__restrict__ x, int64_t ldx,
                                                               int x_dt, const void *__restrict__ r,
                                                               int64_t ldr, int r_dt, int s_dt,
@@ -38,18 +56,18 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(const void *__rest
                                                               int w_dt, void *__restrict__ y,
                                                               int64_t ldy, int y_dt, int hidden,
                                                               float eps) {
-  __shared__ float smem[kRowThreads / 64];
+  __shared__ double smem[kRowThreads / 64];
   const int64_t row = blockIdx.x;
   auto in = [&](int i) -> float {
     const float v = load_as_f32(x, row * ldx + i, x_dt);
     return r ? round_through(v + load_as_f32(r, row * ldr + i, r_dt), s_dt) : v;
   };
-  float ss = 0.f;
+  double ss = 0.0;
   for (int i = threadIdx.x; i < hidden; i += kRowThreads) {
     const float v = in(i);
-    ss += v * v;
+    ss += (double)fp32_rounded(v * v);
   }
-  const float total = block_reduce<false>(ss, smem);
+  const float total = (float)block_sum_f64(ss, smem);
   const float rr = 1.0f / sqrtf(total / (float)hidden + eps);
   for (int i = threadIdx.x; i < hidden; i += kRowThreads) {
     const float v = round_through(in(i) * rr, x_dt);
@@ -69,7 +87,7 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_vec_kernel(const uint16_t
                                                                   uint16_t *__restrict__ y, int64_t ldy,
                                                                   int hidden, float eps) {
   using A = Act<DT>;
-  __shared__ float smem[kRowThreads / 64];
+  __shared__ double smem[kRowThreads / 64];
   const int64_t row = blockIdx.x;
   const int nch = hidden / 8;
   const uint16_t *xr = x + row * ldx;
@@ -83,7 +101,7 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_vec_kernel(const uint16_t
   }
   // v = x (+ r, rounded to the dtype)
   float v[VPT][8];
-  float ss = 0.f;
+  double ss = 0.0;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     const uint16_t *h = reinterpret_cast<const uint16_t *>(&xv[j]);
@@ -92,10 +110,10 @@ __global__ __launch_bounds__(kRowThreads) void rmsnorm_vec_kernel(const uint16_t
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       v[j][e] = RES ? A::rnd(A::in(h[e]) + A::in(hr[e])) : A::in(h[e]);
-      if (live) ss += v[j][e] * v[j][e];
+      if (live) ss += (double)(v[j][e] * v[j][e]);  // exact: 16-bit values square exactly in fp32
     }
   }
-  const float total = block_reduce<false>(ss, smem);
+  const float total = (float)block_sum_f64(ss, smem);
   const float rr = 1.0f / sqrtf(total / (float)hidden + eps);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {

@@ -14,8 +14,9 @@
 // Kernels:
 //  * quantize_act_kernel: one workgroup per activation row, the reference's
 //    ops in the activation dtype t, each rounded to t as torch does:
-//      a = max(amax, round_t(1e-5)); xs = round_t(a / 127);
-//      mult = round_t(round_t(1 / a) * 127)   (torch evaluates 127 / a so)
+//      a = max(amax, round_t(1e-5)); xs = round_t(a / c);
+//      mult = round_t(round_t(1 / a) * c)   (torch evaluates c / a so)
+//    with c = act_scale (127 by default), an fp32 value
 //      xq = int8(clamp(rint(round_t(x * mult)), -128, 127)), NaN -> 0
 //  * w8a8_gemm_kernel: the direct-to-LDS pipeline of the W8A16 prefill kernel
 //    with both operands int8 in LDS (128-byte rows = 128 k per K tile, 8 rows
@@ -45,7 +46,7 @@ constexpr int kRowThreads = 256;
 template <int DT>
 __global__ __launch_bounds__(kRowThreads) void quantize_act_kernel(const uint16_t *__restrict__ x, int64_t ldx,
                                                                    int K, int8_t *__restrict__ q, int64_t ldq,
-                                                                   uint16_t *__restrict__ xs) {
+                                                                   uint16_t *__restrict__ xs, float c) {
   using A = Act<DT>;
   __shared__ float smem[kRowThreads / 64];
   const int64_t row = blockIdx.x;
@@ -57,14 +58,14 @@ __global__ __launch_bounds__(kRowThreads) void quantize_act_kernel(const uint16_
   __syncthreads();
   amax = nan_max(nan_max(smem[0], smem[1]), nan_max(smem[2], smem[3]));
   // clamp(min=1e-5) compares against the bound rounded to the tensor dtype
-  // (and keeps NaN); 127 / a is torch's reciprocal(a) * 127, each rounded.
+  // (and keeps NaN); c / a is torch's reciprocal(a) * c, each rounded.
   const float a = nan_max(amax, A::rnd(1e-5f));
-  const float mult = A::rnd(A::rnd(1.0f / a) * 127.0f);
+  const float mult = A::rnd(A::rnd(1.0f / a) * c);
   for (int i = threadIdx.x; i < K; i += kRowThreads) {
     const float r = rintf(A::rnd(A::in(xr[i]) * mult));
     q[row * ldq + i] = r != r ? (int8_t)0 : (int8_t)(int)fminf(fmaxf(r, -128.0f), 127.0f);
   }
-  if (threadIdx.x == 0) xs[row] = A::out(A::rnd(a / 127.0f));
+  if (threadIdx.x == 0) xs[row] = A::out(A::rnd(a / c));
 }
 
 // The same for rows of K % 8 == 0, K <= 2048 * NC elements, 16-byte aligned:
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(kRowThreads) void quantize_act_kernel(const uint16_
 template <int DT, int NC>
 __global__ __launch_bounds__(kRowThreads) void quantize_act_vec_kernel(const uint16_t *__restrict__ x, int64_t ldx,
                                                                        int K, int8_t *__restrict__ q, int64_t ldq,
-                                                                       uint16_t *__restrict__ xs) {
+                                                                       uint16_t *__restrict__ xs, float c) {
   using A = Act<DT>;
   __shared__ float smem[kRowThreads / 64];
   const int64_t row = blockIdx.x;
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(kRowThreads) void quantize_act_vec_kernel(const uin
   __syncthreads();
   amax = nan_max(nan_max(smem[0], smem[1]), nan_max(smem[2], smem[3]));
   const float a = nan_max(amax, A::rnd(1e-5f));
-  const float mult = A::rnd(A::rnd(1.0f / a) * 127.0f);
+  const float mult = A::rnd(A::rnd(1.0f / a) * c);
   int8_t *qr = q + row * ldq;
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(kRowThreads) void quantize_act_vec_kernel(const uin
     }
     store8(qr + 8 * c, packed[0], packed[1]);
   }
-  if (threadIdx.x == 0) xs[row] = A::out(A::rnd(a / 127.0f));
+  if (threadIdx.x == 0) xs[row] = A::out(A::rnd(a / c));
 }
 
 // One output per thread, exact int32 sums; any K and layout.
@@ -524,19 +525,19 @@ static void launch_dt(const W8A8Args &a, hipStream_t s) {
 namespace w8a8 {
 template <int DT>
 static bool quantize_act_vec(const uint16_t *x, int64_t ldx, int64_t M, int64_t K, int8_t *q, int64_t ldq,
-                             uint16_t *xs, hipStream_t s) {
+                             uint16_t *xs, float c, hipStream_t s) {
   if (K % 8 != 0 || ldx % 8 != 0 || ldq % 8 != 0 || (reinterpret_cast<uintptr_t>(x) & 15) ||
       (reinterpret_cast<uintptr_t>(q) & 7))
     return false;
   const dim3 grid((unsigned)M), block(kRowThreads);
   const int64_t per = 8 * kRowThreads;  // elements per chunk slot
-  if (K <= per) hipLaunchKernelGGL((quantize_act_vec_kernel<DT, 1>), grid, block, 0, s, x, ldx, (int)K, q, ldq, xs);
+  if (K <= per) hipLaunchKernelGGL((quantize_act_vec_kernel<DT, 1>), grid, block, 0, s, x, ldx, (int)K, q, ldq, xs, c);
   else if (K <= 2 * per)
-    hipLaunchKernelGGL((quantize_act_vec_kernel<DT, 2>), grid, block, 0, s, x, ldx, (int)K, q, ldq, xs);
+    hipLaunchKernelGGL((quantize_act_vec_kernel<DT, 2>), grid, block, 0, s, x, ldx, (int)K, q, ldq, xs, c);
   else if (K <= 4 * per)
-    hipLaunchKernelGGL((quantize_act_vec_kernel<DT, 4>), grid, block, 0, s, x, ldx, (int)K, q, ldq, xs);
+    hipLaunchKernelGGL((quantize_act_vec_kernel<DT, 4>), grid, block, 0, s, x, ldx, (int)K, q, ldq, xs, c);
   else if (K <= 8 * per)
-    hipLaunchKernelGGL((quantize_act_vec_kernel<DT, 8>), grid, block, 0, s, x, ldx, (int)K, q, ldq, xs);
+    hipLaunchKernelGGL((quantize_act_vec_kernel<DT, 8>), grid, block, 0, s, x, ldx, (int)K, q, ldq, xs, c);
   else
     return false;
   return true;
@@ -544,17 +545,17 @@ static bool quantize_act_vec(const uint16_t *x, int64_t ldx, int64_t M, int64_t 
 }  // namespace w8a8
 
 hipError_t quantize_act_launch(const void *x, int64_t ldx, int x_dt, int64_t M, int64_t K, int8_t *q, int64_t ldq,
-                               void *xs, hipStream_t s) {
+                               void *xs, float c, hipStream_t s) {
   const dim3 grid((unsigned)M), block(w8a8::kRowThreads);
   const uint16_t *xp = static_cast<const uint16_t *>(x);
   uint16_t *sp = static_cast<uint16_t *>(xs);
-  const bool vec = x_dt == RA_F16 ? w8a8::quantize_act_vec<RA_F16>(xp, ldx, M, K, q, ldq, sp, s)
-                                  : w8a8::quantize_act_vec<RA_BF16>(xp, ldx, M, K, q, ldq, sp, s);
+  const bool vec = x_dt == RA_F16 ? w8a8::quantize_act_vec<RA_F16>(xp, ldx, M, K, q, ldq, sp, c, s)
+                                  : w8a8::quantize_act_vec<RA_BF16>(xp, ldx, M, K, q, ldq, sp, c, s);
   if (vec) return hipGetLastError();
   if (x_dt == RA_F16)
-    hipLaunchKernelGGL((w8a8::quantize_act_kernel<RA_F16>), grid, block, 0, s, xp, ldx, (int)K, q, ldq, sp);
+    hipLaunchKernelGGL((w8a8::quantize_act_kernel<RA_F16>), grid, block, 0, s, xp, ldx, (int)K, q, ldq, sp, c);
   else
-    hipLaunchKernelGGL((w8a8::quantize_act_kernel<RA_BF16>), grid, block, 0, s, xp, ldx, (int)K, q, ldq, sp);
+    hipLaunchKernelGGL((w8a8::quantize_act_kernel<RA_BF16>), grid, block, 0, s, xp, ldx, (int)K, q, ldq, sp, c);
   return hipGetLastError();
 }
 

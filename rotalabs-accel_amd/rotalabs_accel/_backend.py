@@ -20,7 +20,7 @@ _lock = threading.Lock()
 _lib = None
 _load_error: str | None = None
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # enum ra_dtype
 F16, BF16, F32 = 0, 1, 2
@@ -49,7 +49,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "ra_swiglu_bias": ([p, p, p, p, i32, p, i64, i64, i32, p], i32),
         "ra_quantize_per_channel": ([p, i64, i32, i64, i64, p, i64, p, p], i32),
         "ra_quantize_rows": ([p, i64, i32, i64, i64, i32, p, i64, p, p], i32),
-        "ra_quantize_act_rows": ([p, i64, i32, i64, i64, p, i64, p, p], i32),
+        "ra_quantize_act_rows": ([p, i64, i32, i64, i64, p, i64, p, f32, p], i32),
         "ra_w8a8_gemm": ([p, i64, p, p, i64, p, p, i32, p, i64, i32, i64, i64, i64, p], i32),
     }
     for name, (args, res) in sig.items():

@@ -55,6 +55,34 @@ def _rows(t: torch.Tensor, align: int) -> tuple[torch.Tensor, int]:
     return t, ld
 
 
+_KERNEL_BIAS_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def _split_bias(bias: Optional[torch.Tensor], N: int):
+    """Split ``bias`` into (kernel_bias, post_bias).
+
+    The kernels read a contiguous [N] bias at every output column n < N and
+    add it to the fp32 accumulator. The reference adds the bias by
+    broadcasting (``y = y + bias`` on the 2-D output, gemm.py:181-182), so
+    any shape that broadcasts to [M, N] is legal there:
+
+    * a bias holding exactly N values along its last dimension (shape (N,),
+      (1, N), ...) of a kernel dtype goes to the kernel;
+    * a one-element bias is expanded to [N] for the kernel;
+    * anything else is returned as ``post_bias``, to be added to the GEMM
+      output by broadcasting (torch raises for shapes that do not
+      broadcast, as ``y + bias`` does in the reference).
+    """
+    if bias is None:
+        return None, None
+    if bias.dtype in _KERNEL_BIAS_DTYPES:
+        if bias.dim() >= 1 and bias.shape[-1] == N and bias.numel() == N:
+            return bias.reshape(N).contiguous(), None
+        if bias.numel() == 1:
+            return bias.reshape(1).expand(N).contiguous(), None
+    return None, bias
+
+
 def _int8_gemm_hip(x: torch.Tensor, weight_int8: torch.Tensor, scale: torch.Tensor,
                    bias: Optional[torch.Tensor], variant: int = _backend.VARIANT_AUTO) -> torch.Tensor:
     lib = _backend.load()
@@ -68,16 +96,16 @@ def _int8_gemm_hip(x: torch.Tensor, weight_int8: torch.Tensor, scale: torch.Tens
     M = x2.shape[0]
     w, ldw = _rows(weight_int8, align=16)
     s = scale if (scale.dtype == torch.float32 and scale.is_contiguous()) else scale.float().contiguous()
-    b_ptr, b_dt = None, _backend.F32
-    if bias is not None:
-        b = bias.contiguous()
-        b_ptr, b_dt = b.data_ptr(), _backend.dtype_code(b.dtype)
+    b, post_bias = _split_bias(bias, N)
+    b_ptr, b_dt = (None, _backend.F32) if b is None else (b.data_ptr(), _backend.dtype_code(b.dtype))
     y = torch.empty((M, N), dtype=x.dtype, device=dev)
     with _backend.on_device(dev):
         code = lib.ra_w8a16_gemm_ex(
             x2.data_ptr(), ldx, xdt, w.data_ptr(), ldw, s.data_ptr(), b_ptr, b_dt,
             y.data_ptr(), N, M, N, K, variant, _backend.stream_handle(dev))
     _backend.check(code)
+    if post_bias is not None:
+        y.add_(post_bias)
     return y.view(*x.shape[:-1], N)
 
 

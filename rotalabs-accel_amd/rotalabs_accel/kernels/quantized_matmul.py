@@ -43,16 +43,11 @@ W8A8_MIN_M = 17
 ACT_SCALE = 127.0
 
 
-def _check_act_scale(act_scale: float) -> None:
-    if act_scale != ACT_SCALE:
-        raise ValueError(f"W8A8 route: act_scale must be {ACT_SCALE} (int8 range), got {act_scale}")
-
-
-def _quantize_activations_torch(x2: torch.Tensor):
+def _quantize_activations_torch(x2: torch.Tensor, act_scale: float):
     """The reference's ops (quantized_matmul.py:85-87), x_scale in x's dtype."""
     absmax = x2.abs().amax(dim=1, keepdim=True).clamp(min=1e-5)
-    x_scale = (absmax / ACT_SCALE).to(x2.dtype)
-    q = (x2 * (ACT_SCALE / absmax)).round().clamp(-128, 127).to(torch.int8)
+    x_scale = (absmax / act_scale).to(x2.dtype)
+    q = (x2 * (act_scale / absmax)).round().clamp(-128, 127).to(torch.int8)
     return q, x_scale.reshape(-1)
 
 
@@ -60,14 +55,17 @@ def quantize_activations(x: torch.Tensor, act_scale: float = ACT_SCALE):
     """Per-row symmetric int8 quantisation of activations ``x`` (..., K).
 
     Returns ``(x_int8, x_scale)``: int8 (M, K) and the per-row scale (M,) in
-    x's dtype, M = x.numel() // K, with ``x ~= x_int8 * x_scale[:, None]``.
-    GPU tensors (fp16 / bf16) run ``ra_quantize_act_rows``.
+    x's dtype, M = x.numel() // K, with ``x ~= x_int8 * x_scale[:, None]``:
+    ``x_scale = absmax / act_scale`` and ``x_int8 = round(x * (act_scale /
+    absmax))`` clamped to [-128, 127], as quantized_matmul.py:85-87. GPU
+    tensors (fp16 / bf16) run ``ra_quantize_act_rows``, which rounds every
+    step as torch does on the CPU (``act_scale`` taken as an fp32 value; for
+    127, the default, CPU and GPU torch agree).
     """
-    _check_act_scale(act_scale)
     K = x.shape[-1]
     x2 = x.reshape(-1, K)
     if not x.is_cuda:
-        return _quantize_activations_torch(x2)
+        return _quantize_activations_torch(x2, act_scale)
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise TypeError(f"W8A8 route: activations must be float16 or bfloat16 on the GPU, got {x.dtype}")
     lib = _backend.load()
@@ -77,7 +75,7 @@ def quantize_activations(x: torch.Tensor, act_scale: float = ACT_SCALE):
     xs = torch.empty((M,), dtype=x.dtype, device=x.device)
     with _backend.on_device(x.device):
         _backend.check(lib.ra_quantize_act_rows(xr.data_ptr(), ldx, _backend.dtype_code(x.dtype), M, K,
-                                                q.data_ptr(), K, xs.data_ptr(),
+                                                q.data_ptr(), K, xs.data_ptr(), float(act_scale),
                                                 _backend.stream_handle(x.device)))
     return q, xs
 
@@ -124,15 +122,15 @@ def w8a8_gemm(
     w, ldw = _gemm._rows(weight_int8, align=16)
     xs = x_scale.contiguous()
     s = scale if (scale.dtype == torch.float32 and scale.is_contiguous()) else scale.float().contiguous()
-    b_ptr, b_dt = None, _backend.F32
-    if bias is not None:
-        b = bias.contiguous()
-        b_ptr, b_dt = b.data_ptr(), _backend.dtype_code(b.dtype)
+    b, post_bias = _gemm._split_bias(bias, N)
+    b_ptr, b_dt = (None, _backend.F32) if b is None else (b.data_ptr(), _backend.dtype_code(b.dtype))
     y = torch.empty((M, N), dtype=out_dtype, device=dev)
     with _backend.on_device(dev):
         _backend.check(lib.ra_w8a8_gemm(xq.data_ptr(), ldxq, xs.data_ptr(), w.data_ptr(), ldw, s.data_ptr(),
                                         b_ptr, b_dt, y.data_ptr(), N, _backend.dtype_code(out_dtype), M, N, K,
                                         _backend.stream_handle(dev)))
+    if post_bias is not None:
+        y.add_(post_bias)
     return y
 
 

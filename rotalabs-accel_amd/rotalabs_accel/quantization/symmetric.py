@@ -114,6 +114,10 @@ def calculate_quantization_error(
     }
 
 
+_TORCH_DTYPE_NAMES = {torch.float32: "Float", torch.float16: "Half", torch.bfloat16: "BFloat16",
+                      torch.float64: "Double"}
+
+
 class QuantizedLinear(torch.nn.Module):
     """Linear layer with int8 per-channel weights (reference: symmetric.py:210-317).
 
@@ -145,6 +149,14 @@ class QuantizedLinear(torch.nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if not self._quantized:
             raise RuntimeError("Weights not quantized. Call quantize_weights() first.")
+        # The reference runs F.linear(x, dequantize(..., dtype=x.dtype), bias)
+        # (symmetric.py:288-291), which rejects a bias whose dtype differs
+        # from x's -- e.g. this module's fp32 bias with fp16/bf16 activations
+        # -- on every device; the same error is raised here before the GEMM.
+        if self.bias is not None and self.bias.dtype != x.dtype:
+            raise RuntimeError(f"self and mat2 must have the same dtype, but got "
+                               f"{_TORCH_DTYPE_NAMES.get(self.bias.dtype, self.bias.dtype)} and "
+                               f"{_TORCH_DTYPE_NAMES.get(x.dtype, x.dtype)}")
         from rotalabs_accel.kernels.gemm import int8_gemm
         return int8_gemm(x, self.weight_int8, self.weight_scale, self.bias)
 

@@ -80,11 +80,11 @@ def test_w8a8_argument_checks_without_device_work():
     buf = ctypes.create_string_buffer(256)
     p = ctypes.addressof(buf)
     # activation quantisation: fp16 / bf16 only, K = 0 rejected, M = 0 a no-op
-    assert lib.ra_quantize_act_rows(p, 16, 2, 4, 16, p, 16, p, n) == 2
-    assert lib.ra_quantize_act_rows(p, 16, 0, 4, 0, p, 16, p, n) == 1
-    assert lib.ra_quantize_act_rows(n, 0, 0, 0, 16, n, 0, n, n) == 0
-    assert lib.ra_quantize_act_rows(p, 8, 0, 4, 16, p, 16, p, n) == 1      # ldx < K
-    assert lib.ra_quantize_act_rows(p, 16, 0, -1, 16, p, 16, p, n) == 1
+    assert lib.ra_quantize_act_rows(p, 16, 2, 4, 16, p, 16, p, 127.0, n) == 2
+    assert lib.ra_quantize_act_rows(p, 16, 0, 4, 0, p, 16, p, 127.0, n) == 1
+    assert lib.ra_quantize_act_rows(n, 0, 0, 0, 16, n, 0, n, 127.0, n) == 0
+    assert lib.ra_quantize_act_rows(p, 8, 0, 4, 16, p, 16, p, 127.0, n) == 1      # ldx < K
+    assert lib.ra_quantize_act_rows(p, 16, 0, -1, 16, p, 16, p, 127.0, n) == 1
     # int8 GEMM: output dtype fp16 / bf16, bias dtype checked, leading dims
     assert lib.ra_w8a8_gemm(p, 16, p, p, 16, p, n, 0, p, 16, 2, 4, 4, 16, n) == 2
     assert lib.ra_w8a8_gemm(p, 16, p, p, 16, p, p, 9, p, 16, 0, 4, 4, 16, n) == 2

@@ -249,6 +249,64 @@ def test_bias_dtype_mismatch_raises_on_cpu():
         ra.int8_gemm(x, w, torch.ones(8), torch.zeros(8))
 
 
+def test_reexported_names():
+    """The import paths of the reference's re-export lists for this path
+    (src/rotalabs_accel/__init__.py:34-70, kernels/__init__.py:38-42,
+    modules/__init__.py:7-11, quantization/__init__.py:6-12)."""
+    import rotalabs_accel.kernels as K
+    import rotalabs_accel.modules as Mo
+    import rotalabs_accel.quantization as Q
+    for name in ("rmsnorm", "rmsnorm_torch", "TritonRMSNorm", "swiglu_fused", "swiglu_torch", "SwiGLU",
+                 "int8_gemm", "int8_gemm_torch", "Int8Linear", "quantize_symmetric", "dequantize",
+                 "quantize_weight_per_channel", "calculate_quantization_error", "QuantizedLinear"):
+        assert hasattr(ra, name), name
+    for name in ("rmsnorm", "rmsnorm_torch", "rmsnorm_residual_fused", "TritonRMSNorm", "swiglu_fused",
+                 "swiglu_torch", "SwiGLU", "int8_gemm", "int8_gemm_torch", "Int8Linear", "HAS_TRITON"):
+        assert hasattr(K, name), name
+    for name in ("TritonRMSNorm", "SwiGLU", "Int8Linear", "QuantizedLinear"):
+        assert hasattr(Mo, name) and name in Mo.__all__, name
+    assert Mo.SwiGLU is ra.SwiGLU
+    for name in ("quantize_symmetric", "dequantize", "quantize_weight_per_channel",
+                 "calculate_quantization_error", "QuantizedLinear"):
+        assert hasattr(Q, name), name
+
+
+def test_quantized_linear_bias_dtype_error():
+    """QuantizedLinear keeps the reference's fp32 bias; with fp16/bf16
+    activations the reference's F.linear rejects it (symmetric.py:288-291).
+    The same RuntimeError on every device; fp32 activations work."""
+    lin = torch.nn.Linear(32, 16, bias=True)
+    m = ra.QuantizedLinear.from_linear(lin)
+    for dt in (torch.float16, torch.bfloat16):
+        x = torch.randn(3, 32).to(dt)
+        w = ra.dequantize(m.weight_int8, m.weight_scale, dtype=dt, dim=0)
+        with pytest.raises(RuntimeError) as ref_err:
+            torch.nn.functional.linear(x, w, m.bias)
+        with pytest.raises(RuntimeError) as err:
+            m(x)
+        assert str(err.value) == str(ref_err.value)
+    y = m(torch.randn(3, 32))
+    assert y.dtype == torch.float32 and y.shape == (3, 16)
+
+
+def test_split_bias_shapes():
+    """Bias shapes the reference's broadcast add accepts (gemm.py:181-182):
+    (N,) and N values along the last dim go to the kernels, one value is
+    expanded, other broadcastable shapes are added after the GEMM."""
+    from rotalabs_accel.kernels.gemm import _split_bias
+    N = 8
+    for b in (torch.randn(N), torch.randn(1, N), torch.randn(N).half()):
+        kb, post = _split_bias(b, N)
+        assert post is None and kb.shape == (N,) and torch.equal(kb, b.reshape(N))
+    for b in (torch.tensor(2.0), torch.tensor([2.0])):
+        kb, post = _split_bias(b, N)
+        assert post is None and kb.shape == (N,) and (kb == 2.0).all()
+    for b in (torch.randn(3, N), torch.randn(3, 1), torch.randn(N).double()):
+        kb, post = _split_bias(b, N)
+        assert kb is None and post is b
+    assert _split_bias(None, N) == (None, None)
+
+
 @pytest.mark.parametrize("cls", [ra.Int8Linear, ra.QuantizedLinear])
 def test_unquantized_forward_raises(cls):
     with pytest.raises(RuntimeError, match="Weights not quantized"):
@@ -329,8 +387,12 @@ def test_w8a8_route_cpu_matches_oracle(tdt, dt):
     assert rel < 0.05
     small = qm.int8_gemm(x[:, :8], q, s, b, use_cublas=True)
     torch.testing.assert_close(small, ra.int8_gemm(x[:, :8], q, s, b), rtol=0, atol=0)
-    with pytest.raises(ValueError):
-        qm.quantize_activations(x, act_scale=100.0)
+    # act_scale other than 127: the reference's expression with that constant
+    for c in (100.0, 63.5):
+        xq_c, xs_c = qm.quantize_activations(x, act_scale=c)
+        q_o, xs_o = oq.quantize_activations_rows(x.reshape(-1, K).float().numpy(), dt, act_scale=c)
+        np.testing.assert_array_equal(xq_c.numpy(), q_o)
+        np.testing.assert_array_equal(xs_c.float().numpy(), xs_o)
 
 
 def test_swiglu_module_and_bias_cpu():
@@ -350,3 +412,12 @@ def test_swiglu_module_and_bias_cpu():
         sw.swiglu_with_bias(gate, up[..., :32], bg, bu)
     with pytest.raises(AssertionError):
         sw.swiglu_with_bias(gate, up, bg[:32], bu)
+
+
+def test_plumbing_fixture_is_the_reference_output(golden_digests):
+    """tests/golden/plumbing_y_f16.npy (written by make_plumbing.py) carries
+    the reference's config-1 output: its sha256 is the reference's digest."""
+    bits = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "plumbing_y_f16.npy"))
+    assert bits.dtype == np.int16 and bits.shape == (16, 4096)
+    assert hashlib.sha256(bits.tobytes()).hexdigest() == golden_digests["y_f16"]
+    assert np.array_equal(bits[0, :8].view(np.float16).astype(np.float64), golden_digests["y_first8"])

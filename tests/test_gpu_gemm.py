@@ -234,6 +234,35 @@ def test_bias_dtypes(gpu, bdt):
     np.testing.assert_allclose(y.double().numpy(), ref, rtol=2e-3, atol=2e-3)
 
 
+def test_bias_shapes(gpu):
+    """Bias shapes the reference's broadcast add (y + bias, gemm.py:181-182)
+    accepts: a scalar and a one-element bias are expanded to [N] for the
+    kernels, (1, N) goes to the kernels, (M, N) and (M, 1) are added after
+    the GEMM; a shape that does not broadcast raises (as y + bias does);
+    the W8A8 route takes the same shapes."""
+    from rotalabs_accel.kernels import quantized_matmul as qm
+    M, K, N = 24, 512, 200
+    c = gemm_case(M, K, N, seed=21)
+    x, q, s = c.x.to(gpu), c.q.to(gpu), c.s.to(gpu)
+    y0 = ra.int8_gemm(x, q, s).float()
+    xq, xs = qm.quantize_activations(x)
+    w0 = qm.w8a8_gemm(xq, xs, q, s).float()
+    g = torch.Generator().manual_seed(3)
+    for shape in [(), (1,), (1, N), (M, N), (M, 1)]:
+        b = (torch.randn(shape, generator=g) * 0.5).half().to(gpu)
+        print(f"  bias shape {shape}", flush=True)
+        y = ra.int8_gemm(x, q, s, b)
+        torch.cuda.synchronize()
+        assert y.shape == (M, N) and y.dtype == torch.float16
+        torch.testing.assert_close(y.float(), (y0 + b.float()).half().float(), rtol=2e-3, atol=2e-3)
+        w = qm.w8a8_gemm(xq, xs, q, s, b)
+        torch.testing.assert_close(w.float(), (w0 + b.float()).half().float(), rtol=2e-3, atol=2e-3)
+    for bad in [(N + 1,), (N - 1,), (M + 1, N)]:
+        b = torch.zeros(bad, dtype=torch.float16, device=gpu)
+        with pytest.raises(RuntimeError):
+            ra.int8_gemm(x, q, s, b)
+
+
 def test_strided_and_misaligned_inputs(gpu):
     c = gemm_case(24, 512, 200, seed=8)
     xb = torch.zeros(24, 520, dtype=torch.float16)
@@ -305,8 +334,17 @@ def test_batched_leading_dims_and_modules(gpu):
     torch.testing.assert_close(y.reshape(-1, 320).float(), ref.float(), rtol=1e-2, atol=1e-2)
     qm = ra.QuantizedLinear.from_linear(lin).to(gpu)
     qm._quantized = True
+    # the module's fp32 bias with fp16 activations: the reference's F.linear
+    # error (symmetric.py:288-291), as on the CPU
+    with pytest.raises(RuntimeError, match="same dtype"):
+        qm(x.to(gpu))
+    qm.bias.data = qm.bias.data.half()
     yq = qm(x.to(gpu)).cpu()
     torch.testing.assert_close(yq.float(), y.float(), rtol=2e-3, atol=2e-3)
+    # fp32 activations with the fp32 bias run (the generic kernel)
+    qm.bias.data = qm.bias.data.float()
+    y32 = qm(x.float().to(gpu)).cpu()
+    torch.testing.assert_close(y32, y.float(), rtol=2e-3, atol=2e-3)
 
 
 def test_empty_and_k_tail(gpu):

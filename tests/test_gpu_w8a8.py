@@ -62,6 +62,21 @@ def test_quantize_activations_bit_exact(gpu, dt, M, K):
     assert xs.dtype == dt and q.shape == (M, K)
 
 
+@pytest.mark.parametrize("c", [100.0, 63.5])
+@pytest.mark.parametrize("M,K", [(5, 7), (17, 4096), (3, 16392)])
+def test_quantize_activations_other_act_scale(gpu, c, M, K):
+    """act_scale other than 127 (quantized_matmul.py:48): bit-exact with the
+    oracle, which follows torch's CPU evaluation of the reference's ops."""
+    for dt in (torch.float16, torch.bfloat16):
+        print(f"  act-quant M={M} K={K} dt={dt} act_scale={c}", flush=True)
+        x = _acts(M, K, dt, seed=M + K + 1)
+        q, xs = qm.quantize_activations(x.to(gpu), act_scale=c)
+        torch.cuda.synchronize()
+        q_ref, xs_ref = oq.quantize_activations_rows(x.float().numpy(), DT[dt], act_scale=c)
+        np.testing.assert_array_equal(q.cpu().numpy(), q_ref)
+        np.testing.assert_array_equal(_np(xs), xs_ref)
+
+
 def test_quantize_activations_strided_rows(gpu):
     x = _acts(40, 512, torch.float16, seed=5)
     store = torch.zeros(40, 520, dtype=torch.float16, device=gpu)

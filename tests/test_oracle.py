@@ -193,6 +193,44 @@ def test_dequantize_closed_form():
     assert np.array_equal(refb.float().numpy(), oq.dequantize(q, s, "bf16"))
 
 
+@pytest.mark.parametrize("tdt,dt", [(torch.bfloat16, "bf16"), (torch.float16, "f16")])
+def test_rmsnorm_exact_oracle_pinned(golden, tdt, dt):
+    """rmsnorm_exact_ref (normalization.py:43-45 with exactly rounded fp32
+    ops) is pinned three ways:
+    * rows whose fp32 sum of squares is exact in any order (multiples of 1/8
+      up to 4 in magnitude; a row of +-2^-10, where eps is half the mean):
+      equal bit for bit to torch's evaluation of the fallback;
+    * random rows (the golden vectors' and wider ones): equal to torch's on
+      all but a sliver (torch's fp32 sum rounds in its own order) and within
+      one output ulp everywhere;
+    * a float64 closed form x * w / sqrt(mean(x^2) + eps) within two output
+      ulps (a dropped eps, a wrong divisor or a missing rounding fails one
+      of these)."""
+    from oracle.quant import round_to
+    g = torch.Generator().manual_seed(9)
+    H = 8192
+    exact = (torch.randint(-32, 33, (6, H), generator=g).float() / 8)
+    exact[5] = torch.where(torch.rand(H, generator=g) < 0.5, -1.0, 1.0) * 2.0 ** -10
+    x = exact.to(tdt)
+    w = (1 + 0.01 * torch.randn(H, generator=g)).to(tdt)
+    got = fallback.rmsnorm_exact_ref(x.float().numpy(), w.float().numpy(), 1e-6, dt)
+    np.testing.assert_array_equal(got, fallback.rmsnorm_ref(x, w, 1e-6).float().numpy())
+    ulp = 2.0 ** -7 if dt == "bf16" else 2.0 ** -10
+    rand = [(torch.randn(64, H, generator=g) * 2).to(tdt)]
+    if dt == "bf16":
+        rand.append(_t16(golden["rms_x_bf16"], tdt))
+    for xr in rand:
+        wr = (1 + 0.01 * torch.randn(xr.shape[-1], generator=g)).to(tdt)
+        got = fallback.rmsnorm_exact_ref(xr.float().numpy(), wr.float().numpy(), 1e-6, dt)
+        tor = fallback.rmsnorm_ref(xr, wr, 1e-6).float().numpy()
+        assert (got == tor).mean() > 0.999
+        np.testing.assert_allclose(got, tor, rtol=ulp, atol=0)
+        x64 = xr.double().numpy()
+        closed = x64 * wr.double().numpy() / np.sqrt((x64 * x64).mean(-1, keepdims=True) + 1e-6)
+        np.testing.assert_allclose(got, closed, rtol=2 * ulp, atol=2.0 ** -24)   # fp16 subnormal step
+        assert np.array_equal(got, round_to(got, dt))
+
+
 def test_rmsnorm_residual_oracle_pinned(golden):
     """rmsnorm_residual_ref (normalization.py:48-64) pinned by identities:
     a zero residual is rmsnorm of x; with equal dtypes it is rmsnorm of the
@@ -286,6 +324,21 @@ def test_w8a8_activation_quant_oracle_pinned(tdt, dt):
     assert (np.abs(q[fin].astype(int)).max(1) >= 126).all()
     assert (q[1] == 0).all() and np.isnan(xs[1]) and np.isinf(xs[2]) and (q[2] == 0).all()
     assert (q[5] == -127).all()
+
+
+@pytest.mark.parametrize("c", [100.0, 63.5, 200.0])
+def test_w8a8_activation_quant_general_act_scale(c):
+    """The restatement with another act_scale equals torch's CPU evaluation of
+    the reference's expression with that constant (quantized_matmul.py:85-87,
+    act_scale argument at :48)."""
+    for tdt, dt in ((torch.float16, "f16"), (torch.bfloat16, "bf16")):
+        x = _act_rows(tdt)
+        absmax = x.abs().amax(dim=1, keepdim=True).clamp(min=1e-5)
+        xs_t = (absmax / c).to(tdt).reshape(-1)
+        q_t = (x * (c / absmax)).round().clamp(-128, 127).to(torch.int8)
+        q, xs = oq.quantize_activations_rows(x.float().numpy(), dt, act_scale=c)
+        np.testing.assert_array_equal(q, q_t.numpy())
+        np.testing.assert_array_equal(xs, xs_t.float().numpy())
 
 
 def test_w8a8_scalar_division_forms_agree():
