@@ -103,17 +103,29 @@ def copy_calibration():
 
 
 class GemmLauncher:
-    """Pre-bound ra_w8a16_gemm calls (C ABI), one per weight copy, launched on
-    torch's current stream (so they can be captured into a HIP graph)."""
+    """Pre-bound ra_w8a16_gemm_ws calls (C ABI), one per weight copy, launched
+    on torch's current stream (so they can be captured into a HIP graph),
+    with a zero-filled workspace of the size the library asks for (the
+    split-K small-batch kernel keeps its partial sums there)."""
 
-    def __init__(self, x, weights, scale, y):
+    def __init__(self, x, weights, scale, y, variant=0):
+        import torch
         from rotalabs_accel import _backend
-        self.fn = _backend.load().ra_w8a16_gemm
+        lib = _backend.load()
         M, K = x.shape
         N = weights[0].shape[0]
         xdt = _backend.dtype_code(x.dtype)
-        self.args = [(x.data_ptr(), K, xdt, w.data_ptr(), K, scale.data_ptr(), None, 0,
-                      y.data_ptr(), N, M, N, K) for w in weights]
+        nws = int(lib.ra_w8a16_gemm_workspace_size(M, N, K, xdt))
+        self.ws = torch.zeros(max(nws, 1), dtype=torch.uint8, device=x.device)
+        wsp = self.ws.data_ptr() if nws else None
+        if variant:
+            self.fn = lib.ra_w8a16_gemm_ex
+            self.args = [(x.data_ptr(), K, xdt, w.data_ptr(), K, scale.data_ptr(), None, 0,
+                          y.data_ptr(), N, M, N, K, variant, wsp, nws) for w in weights]
+        else:
+            self.fn = lib.ra_w8a16_gemm_ws
+            self.args = [(x.data_ptr(), K, xdt, w.data_ptr(), K, scale.data_ptr(), None, 0,
+                          y.data_ptr(), N, M, N, K, wsp, nws) for w in weights]
         self.keep = (x, weights, scale, y)
 
     def run(self, steps: int):
@@ -123,7 +135,7 @@ class GemmLauncher:
         for i in range(steps):
             rc = fn(*args[i % n], stream)
             if rc:
-                raise RuntimeError(f"ra_w8a16_gemm failed with {rc}")
+                raise RuntimeError(f"ra_w8a16_gemm_ws failed with {rc}")
 
 
 def time_eager(launcher, steps: int, warmup: int):
@@ -194,10 +206,10 @@ def cpu_baseline(M, K, N, seed, budget_s):
             "gbs": gemm_bytes(M, K, N) / med / 1e9, "tflops": gemm_flops(M, K, N) / med / 1e12}
 
 
-VARIANT_NAMES = {1: "skinny", 2: "tiled", 3: "generic", 4: "gemv", 5: "rows", 6: "batch"}
+VARIANT_NAMES = {1: "skinny", 2: "tiled", 3: "generic", 4: "gemv", 5: "rows", 6: "batch", 7: "splitk"}
 # Kernel (symbol prefix in rocprofv3 traces) that each variant launches.
 VARIANT_KERNELS = {1: "skinny_kernel", 2: "tiled_dma_kernel", 3: "generic_kernel", 4: "gemv_kernel",
-                   5: "gemv_rows_lds_kernel", 6: "batch_kernel"}
+                   5: "gemv_rows_lds_kernel", 6: "batch_kernel", 7: "splitk_kernel"}
 
 
 def run_decode(args, dev):

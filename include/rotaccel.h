@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define RA_ABI_VERSION 5
+#define RA_ABI_VERSION 6
 
 enum ra_dtype { RA_F16 = 0, RA_BF16 = 1, RA_F32 = 2 };
 
@@ -35,7 +35,8 @@ enum ra_status {
   RA_ERR_DTYPE = 2,     /* unsupported dtype combination                      */
   RA_ERR_LAUNCH = 3,    /* kernel launch failed (hipGetLastError != success)  */
   RA_ERR_VARIANT = 4,   /* a forced kernel variant cannot run this shape      */
-  RA_ERR_DEVICE = 5     /* no usable device / not a gfx950 device             */
+  RA_ERR_DEVICE = 5,    /* no usable device / not a gfx950 device             */
+  RA_ERR_WORKSPACE = 6  /* workspace smaller than the problem needs           */
 };
 
 /* Kernel variants for ra_w8a16_gemm_ex. RA_VARIANT_AUTO picks by shape. */
@@ -46,7 +47,11 @@ enum ra_variant {
   RA_VARIANT_GENERIC = 3, /* any shape / alignment / dtype, VALU, slow        */
   RA_VARIANT_GEMV = 4,    /* decode GEMV, M <= 4, x staged in LDS             */
   RA_VARIANT_ROWS = 5,    /* decode row GEMV, M <= 2, one weight row per wave */
-  RA_VARIANT_BATCH = 6    /* small batch, M <= 64, K % 128 == 0, MFMA + LDS */
+  RA_VARIANT_BATCH = 6,   /* small batch, M <= 64, K % 128 == 0, MFMA + LDS */
+  RA_VARIANT_SPLITK = 7,  /* small batch, M <= 64, K % 128 == 0, split K      */
+  RA_VARIANT_SPLITK_SPREAD = 8 /* the same with a row block's K splits run on
+                                  different XCDs (tests the exchange of the
+                                  partial sums across XCDs)                  */
 };
 
 /* Version of this ABI (RA_ABI_VERSION of the built library). */
@@ -80,16 +85,40 @@ int ra_w8a16_gemm(const void *x, int64_t ldx, int x_dtype,
                   void *y, int64_t ldy,
                   int64_t M, int64_t N, int64_t K, void *stream);
 
-/* ra_w8a16_gemm with an explicit kernel variant (enum ra_variant); used by
+/*
+ * ra_w8a16_gemm with a caller-owned device workspace, which lets the small-
+ * batch kernel (3 <= M <= 64) split K over several workgroups and combine
+ * their fp32 partial sums there in a fixed order (deterministic). Same
+ * parity as ra_w8a16_gemm; it replaces the same reference call.
+ * workspace_bytes must be at least ra_w8a16_gemm_workspace_size(M, N, K,
+ * x_dtype) (RA_ERR_WORKSPACE otherwise); workspace may be NULL (or the size
+ * 0), which runs the kernels that need none, as ra_w8a16_gemm does.
+ * The workspace must be zero-filled before its first use; every call leaves
+ * it ready for the next one (its counters back at zero). Calls that may run
+ * concurrently (other streams) need workspaces of their own.
+ */
+int ra_w8a16_gemm_ws(const void *x, int64_t ldx, int x_dtype,
+                     const int8_t *w, int64_t ldw, const float *scale,
+                     const void *bias, int bias_dtype,
+                     void *y, int64_t ldy,
+                     int64_t M, int64_t N, int64_t K,
+                     void *workspace, size_t workspace_bytes, void *stream);
+
+/* Workspace bytes ra_w8a16_gemm_ws may use for this problem (0: none). */
+size_t ra_w8a16_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int x_dtype);
+
+/* ra_w8a16_gemm_ws with an explicit kernel variant (enum ra_variant); used by
  * tests to run every kernel on the same inputs. Returns RA_ERR_VARIANT if the
  * forced variant cannot handle the shape, dtype or alignment. */
 int ra_w8a16_gemm_ex(const void *x, int64_t ldx, int x_dtype,
                      const int8_t *w, int64_t ldw, const float *scale,
                      const void *bias, int bias_dtype,
                      void *y, int64_t ldy,
-                     int64_t M, int64_t N, int64_t K, int variant, void *stream);
+                     int64_t M, int64_t N, int64_t K, int variant,
+                     void *workspace, size_t workspace_bytes, void *stream);
 
-/* Which variant RA_VARIANT_AUTO runs for this problem (enum ra_variant). */
+/* Which variant RA_VARIANT_AUTO runs for this problem (enum ra_variant),
+ * given a workspace of ra_w8a16_gemm_workspace_size bytes. */
 int ra_w8a16_gemm_select(int64_t M, int64_t N, int64_t K, int x_dtype);
 
 /*
@@ -106,6 +135,16 @@ int ra_w8a16_gateup_swiglu(const void *x, int64_t ldx, int x_dtype,
                            const int8_t *w, int64_t ldw, const float *scale,
                            void *h, int64_t ldh,
                            int64_t M, int64_t I, int64_t K, void *stream);
+
+/* ra_w8a16_gateup_swiglu with a caller-owned workspace (contract as for
+ * ra_w8a16_gemm_ws; size from ra_w8a16_gateup_workspace_size). */
+int ra_w8a16_gateup_swiglu_ws(const void *x, int64_t ldx, int x_dtype,
+                              const int8_t *w, int64_t ldw, const float *scale,
+                              void *h, int64_t ldh,
+                              int64_t M, int64_t I, int64_t K,
+                              void *workspace, size_t workspace_bytes, void *stream);
+
+size_t ra_w8a16_gateup_workspace_size(int64_t M, int64_t I, int64_t K, int x_dtype);
 
 /*
  * y[r,:] = (x[r,:] * rsqrt(mean(x[r,:]^2) + eps)) rounded to x_dtype, times

@@ -43,9 +43,17 @@ SkinnyCfg skinny_config(int64_t M, int64_t N, int64_t K) {
 // and the skinny split-K kernel is faster).
 constexpr int64_t kSkinnyMaxM = 64;
 
-int select_variant(const GemmArgs &a) {
+// K from which the small-batch GEMM splits K over workgroups (given a
+// workspace). Measured on MI355X (graph replay, weights streamed from HBM):
+// M=17 K=28672 N=8192 47.4 us split vs 50.0 us for the one-pass batch kernel;
+// at K=4096 N=11008 the one-pass kernel is ahead (M=4..64: 11.2-23.5 us vs
+// 15.6-30.2), and at K=8192 N=57344 (88.6 vs 115.6).
+constexpr int64_t kSplitkMinK = 16384;
+
+int select_variant(const GemmArgs &a, bool have_ws) {
   if (a.K == 0) return RA_VARIANT_GENERIC;
   if (gemv_rows_supported(a)) return RA_VARIANT_ROWS;
+  if (have_ws && a.M <= kSkinnyMaxM && a.K >= kSplitkMinK && splitk_supported(a)) return RA_VARIANT_SPLITK;
   // M = 3..64: the small-batch kernel (line-wide weight loads, activations
   // read once per 48 rows) where K % 128 == 0, else the split-K MFMA kernel;
   // both measured faster than the LDS GEMV, which stays as a fallback.
@@ -93,20 +101,39 @@ const char *ra_strerror(int code) {
     case RA_ERR_LAUNCH: return "rotaccel: kernel launch failed";
     case RA_ERR_VARIANT: return "rotaccel: the requested kernel variant cannot run this problem";
     case RA_ERR_DEVICE: return "rotaccel: no usable gfx950 device";
+    case RA_ERR_WORKSPACE: return "rotaccel: workspace smaller than the size the problem needs";
     default: return "rotaccel: unknown error";
   }
 }
 
+size_t ra_w8a16_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int x_dtype) {
+  if (x_dtype != RA_F16 && x_dtype != RA_BF16) return 0;
+  if (M <= 2 || M > kSkinnyMaxM) return 0;  // the row GEMVs and the tiled GEMM need none
+  // (below kSplitkMinK only a forced RA_VARIANT_SPLITK launch uses it)
+  const SplitkPlan p = splitk_plan(M, N, K, false, true);
+  return p.ok ? p.ws_bytes : 0;
+}
+
 int ra_w8a16_gemm_ex(const void *x, int64_t ldx, int x_dtype, const int8_t *w, int64_t ldw,
                      const float *scale, const void *bias, int bias_dtype, void *y, int64_t ldy, int64_t M,
-                     int64_t N, int64_t K, int variant, void *stream) {
+                     int64_t N, int64_t K, int variant, void *workspace, size_t workspace_bytes, void *stream) {
   const GemmArgs a{x, ldx, x_dtype, w, ldw, scale, bias, bias_dtype, y, ldy, M, N, K};
   int st = check_gemm(a);
   if (st != RA_OK) return st;
   if (M == 0 || N == 0) return RA_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  int v = variant == RA_VARIANT_AUTO ? select_variant(a) : variant;
+  const bool have_ws = workspace != nullptr && workspace_bytes > 0;
+  int v = variant == RA_VARIANT_AUTO ? select_variant(a, have_ws) : variant;
   switch (v) {
+    case RA_VARIANT_SPLITK:
+    case RA_VARIANT_SPLITK_SPREAD: {
+      if (!splitk_supported(a) || M > kSkinnyMaxM) return RA_ERR_VARIANT;
+      SplitkPlan p = splitk_plan(M, N, K, false, have_ws);
+      p.spread = v == RA_VARIANT_SPLITK_SPREAD;
+      if (!p.ok) return RA_ERR_VARIANT;
+      if (p.ws_bytes > 0 && workspace_bytes < p.ws_bytes) return RA_ERR_WORKSPACE;
+      return to_status(splitk_launch(a, p, workspace, s));
+    }
     case RA_VARIANT_SKINNY:
       if (!skinny_supported(a) || K == 0) return RA_ERR_VARIANT;
       return to_status(skinny_launch(a, skinny_config(M, N, K), s));
@@ -133,19 +160,40 @@ int ra_w8a16_gemm(const void *x, int64_t ldx, int x_dtype, const int8_t *w, int6
                   const void *bias, int bias_dtype, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                   void *stream) {
   return ra_w8a16_gemm_ex(x, ldx, x_dtype, w, ldw, scale, bias, bias_dtype, y, ldy, M, N, K, RA_VARIANT_AUTO,
-                          stream);
+                          nullptr, 0, stream);
+}
+
+int ra_w8a16_gemm_ws(const void *x, int64_t ldx, int x_dtype, const int8_t *w, int64_t ldw, const float *scale,
+                     const void *bias, int bias_dtype, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                     void *workspace, size_t workspace_bytes, void *stream) {
+  return ra_w8a16_gemm_ex(x, ldx, x_dtype, w, ldw, scale, bias, bias_dtype, y, ldy, M, N, K, RA_VARIANT_AUTO,
+                          workspace, workspace_bytes, stream);
 }
 
 int ra_w8a16_gemm_select(int64_t M, int64_t N, int64_t K, int x_dtype) {
-  // Alignment is assumed satisfied (contiguous, 16-byte aligned operands).
+  // Alignment is assumed satisfied (contiguous, 16-byte aligned operands)
+  // and a workspace of ra_w8a16_gemm_workspace_size bytes given.
   const GemmArgs a{reinterpret_cast<const void *>(256), K, x_dtype, reinterpret_cast<const int8_t *>(256),
                    K, nullptr, nullptr, RA_F32, nullptr, N, M, N, K};
-  return select_variant(a);
+  return select_variant(a, true);
+}
+
+size_t ra_w8a16_gateup_workspace_size(int64_t M, int64_t I, int64_t K, int x_dtype) {
+  if (x_dtype != RA_F16 && x_dtype != RA_BF16) return 0;
+  if (M <= 2 || M > kSkinnyMaxM) return 0;
+  const SplitkPlan p = splitk_plan(M, I, K, true, true);
+  return p.ok ? p.ws_bytes : 0;
 }
 
 int ra_w8a16_gateup_swiglu(const void *x, int64_t ldx, int x_dtype, const int8_t *w, int64_t ldw,
                            const float *scale, void *h, int64_t ldh, int64_t M, int64_t I, int64_t K,
                            void *stream) {
+  return ra_w8a16_gateup_swiglu_ws(x, ldx, x_dtype, w, ldw, scale, h, ldh, M, I, K, nullptr, 0, stream);
+}
+
+int ra_w8a16_gateup_swiglu_ws(const void *x, int64_t ldx, int x_dtype, const int8_t *w, int64_t ldw,
+                              const float *scale, void *h, int64_t ldh, int64_t M, int64_t I, int64_t K,
+                              void *workspace, size_t workspace_bytes, void *stream) {
   if (M < 0 || I < 0 || K < 0 || M > INT32_MAX || 2 * I > INT32_MAX || K > INT32_MAX) return RA_ERR_ARG;
   if (x_dtype != RA_F16 && x_dtype != RA_BF16 && x_dtype != RA_F32) return RA_ERR_DTYPE;
   if (M == 0 || I == 0) return RA_OK;
@@ -153,7 +201,15 @@ int ra_w8a16_gateup_swiglu(const void *x, int64_t ldx, int x_dtype, const int8_t
   if (ldx < K || ldw < K || ldh < I) return RA_ERR_ARG;
   const GateUpArgs a{x, ldx, x_dtype, w, ldw, scale, h, ldh, M, I, K};
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool have_ws = workspace != nullptr && workspace_bytes > 0;
   if (K > 0 && gateup_gemv_rows_supported(a)) return to_status(gateup_gemv_rows_launch(a, s));
+  if (K >= kSplitkMinK && have_ws && M <= kSkinnyMaxM && gateup_splitk_supported(a)) {
+    const SplitkPlan p = splitk_plan(M, I, K, true, true);
+    if (p.ok) {
+      if (p.ws_bytes > 0 && workspace_bytes < p.ws_bytes) return RA_ERR_WORKSPACE;
+      return to_status(gateup_splitk_launch(a, p, workspace, s));
+    }
+  }
   if (K > 0 && M <= kSkinnyMaxM && gateup_batch_supported(a)) return to_status(gateup_batch_launch(a, s));
   if (K > 0 && M <= kSkinnyMaxM && gateup_skinny_supported(a)) return to_status(gateup_skinny_launch(a, s));
   if (K > 0 && gateup_gemv_supported(a)) return to_status(gateup_gemv_launch(a, s));

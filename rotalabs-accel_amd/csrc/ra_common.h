@@ -44,6 +44,45 @@ __device__ __forceinline__ uint4 load_stream16(const void *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// ---------------------------------------------------------------------------
+// Direct-to-LDS copies (gfx950 global_load_lds_dwordx4) and explicit waits.
+// LDS byte address of a __shared__ object (what M0 and ds_* addresses use).
+__device__ __forceinline__ uint32_t lds_offset(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// 16 bytes per lane from global memory to LDS at M0 + OFS + 16 * lane; the
+// instruction offset OFS is added to both the global and the LDS address, so
+// up to four consecutive 1 KB copies share one M0 value (the caller passes
+// g - OFS). NEW_M0 first writes M0; an LDS DMA that reads M0 needs one wait
+// state after that SALU write.
+template <int OFS, bool NEW_M0>
+__device__ __forceinline__ void dma16(const void *g_minus_ofs, uint32_t m0_value) {
+  if (NEW_M0)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off offset:%2" ::"s"(m0_value),
+                 "v"(g_minus_ofs), "n"(OFS)
+                 : "memory", "m0");
+  else
+    asm volatile("global_load_lds_dwordx4 %0, off offset:%1" ::"v"(g_minus_ofs), "n"(OFS) : "memory");
+}
+
+// As dma16 with the uniform part of the global address in an SGPR pair and a
+// 32-bit per-lane byte offset, so a copy needs no per-lane address arithmetic.
+template <int OFS, bool NEW_M0>
+__device__ __forceinline__ void dma16s(const void *sbase, uint32_t voff, uint32_t m0_value) {
+  if (NEW_M0)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3" ::"s"(m0_value),
+                 "v"(voff), "s"(sbase), "n"(OFS)
+                 : "memory", "m0");
+  else
+    asm volatile("global_load_lds_dwordx4 %0, %1 offset:%2" ::"v"(voff), "s"(sbase), "n"(OFS) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [LO, HI).
 template <int LO, int HI, typename F>
 __device__ __forceinline__ void static_for_int(F &&f) {

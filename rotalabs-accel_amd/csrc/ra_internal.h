@@ -2,7 +2,10 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
+
+#include <algorithm>
 
 #include "rotaccel.h"
 
@@ -68,6 +71,21 @@ bool batch_supported(const GemmArgs &a);
 hipError_t batch_launch(const GemmArgs &a, hipStream_t s);
 bool gateup_batch_supported(const GateUpArgs &a);
 hipError_t gateup_batch_launch(const GateUpArgs &a, hipStream_t s);
+
+// Small-batch GEMM with split K (M <= 64, K % 128 == 0): weights and
+// activations staged by direct-to-LDS copies; S > 1 needs a workspace of
+// ws_bytes (a zeroed counter block of cnt_bytes, then the partial sums).
+struct SplitkPlan {
+  bool ok;
+  int mt, tw, S, kc, nb;
+  bool spread;  // a row block's splits on different XCDs (test mode)
+  size_t cnt_bytes, ws_bytes;
+};
+SplitkPlan splitk_plan(int64_t M, int64_t N, int64_t K, bool gu, bool allow_split);
+bool splitk_supported(const GemmArgs &a);
+hipError_t splitk_launch(const GemmArgs &a, const SplitkPlan &p, void *ws, hipStream_t s);
+bool gateup_splitk_supported(const GateUpArgs &a);
+hipError_t gateup_splitk_launch(const GateUpArgs &a, const SplitkPlan &p, void *ws, hipStream_t s);
 
 // Decode GEMV (M <= 4, x staged in LDS, one HBM round trip per wave).
 bool gemv_supported(const GemmArgs &a);

@@ -1,0 +1,431 @@
+// Small-batch W8A16 GEMM with split K (3 <= M <= 64) on gfx950.
+//
+// Replaces the reference's Triton tile loop (src/rotalabs_accel/kernels/
+// gemm.py:113-138) for small batches, where the cost is streaming the N*K
+// weight bytes and every CU must also read the activation block. With one
+// workgroup per CU owning R of the N rows over all of K, each CU reads the
+// whole activation block (M*K*2 bytes, 512 KB at M=64 K=4096) through its
+// address unit for R*K weight bytes (~176 KB): at M=64 activation reads are
+// 2.7x the weight stream. Splitting K over S workgroups lets a workgroup own
+// S times more rows for the same weight bytes, so it reads S times fewer
+// activation bytes; the S partial sums are combined in a fixed order.
+//
+//  * Unit = (row block rb, K split s); a workgroup of 4 waves owns
+//    R = 4*TW*16 output columns (with the gate/up pair, TW gate tiles and the
+//    TW matching up tiles per wave) over K range [s*kc, min(K, (s+1)*kc)).
+//  * Y^T = W . X^T with v_mfma_f32_16x16x32_{f16,bf16}: MFMA rows are weight
+//    rows, MFMA columns activation rows (M padded to 16*MT).
+//  * Both operands reach LDS through direct-to-LDS copies
+//    (global_load_lds_dwordx4), staged 128 k at a time, D stages in flight:
+//    - weights: each wave streams its own 16*NTW rows, 8 rows x 128 bytes per
+//      1 KB copy (full lines, non-temporal), into a wave-private ring. The
+//      16-byte chunks land XOR-swizzled by (row >> 1) & 7 (the swizzle is
+//      applied on the global side: lane l fetches the chunk that belongs at
+//      its LDS slot), so the MFMA operand reads (16 rows, same chunk) are
+//      conflict-free; the int8 values are dequantised exactly in registers.
+//    - activations: the stage's [16*MT, 128] fp16/bf16 block is copied once
+//      per workgroup (4 rows x 256 bytes per copy, chunks swizzled by
+//      row & 15) into a ring of D+1 slots shared by the 4 waves; one barrier
+//      per stage.
+//    No VGPR holds data in flight, so the pipeline depth is set by LDS alone.
+//  * S = 1: the epilogue applies scale (+ bias) or the gate/up SwiGLU to the
+//    fp32 sums and rounds once. S > 1: every unit stores its fp32 partial
+//    sums (fragment order) in the workspace with device-scope stores, waits
+//    for them, then increments its row block's counter (device-scope
+//    atomic); the unit that finds the other S-1 arrived reads their partial
+//    sums with device-scope loads, sums the S partials in split order
+//    0..S-1 (deterministic), runs the epilogue and resets the counter to
+//    zero for the next call. No unit waits for another.
+#include "ra_common.h"
+#include "ra_internal.h"
+
+namespace ra {
+
+namespace sk {
+constexpr int KS = 128;       // k per stage
+constexpr int NW = 4;         // waves per workgroup
+constexpr int kMaxM = 64;
+constexpr int kLds = 159 * 1024;  // rings; the rest holds the reduction flag
+constexpr int kMaxD = 6;
+// Counters of the split combine sit at the start of every workspace, one
+// per row block, in a fixed region (a call never writes partial sums where
+// another plan keeps a counter); plans with more row blocks do not split.
+constexpr int kMaxCounters = 4096;
+constexpr size_t kCounterBytes = kMaxCounters * sizeof(int);
+
+constexpr int ntw(int tw, bool gu) { return gu ? 2 * tw : tw; }
+constexpr int x_slot(int mt) { return mt * 4096; }            // [16*MT rows][256 bytes]
+constexpr int w_slot(int tw, bool gu) { return ntw(tw, gu) * 2048; }  // per wave: [16*NTW rows][128 bytes]
+constexpr int lds_bytes(int mt, int tw, bool gu, int d) { return (d + 1) * x_slot(mt) + d * NW * w_slot(tw, gu); }
+constexpr int copies(int mt, int tw, bool gu) { return 2 * ntw(tw, gu) + mt; }  // per wave per stage
+// Deepest pipeline that fits LDS and the 6-bit vmcnt.
+constexpr int depth(int mt, int tw, bool gu) {
+  int d = kMaxD;
+  while (d > 2 && (lds_bytes(mt, tw, gu, d) > kLds || (d - 1) * copies(mt, tw, gu) > 63)) --d;
+  return d;
+}
+// fp32 values of one unit's partial sums: per wave NTW x MT fragments of 64 lanes x 4.
+constexpr int part_floats(int mt, int tw, bool gu) { return NW * ntw(tw, gu) * mt * 256; }
+}  // namespace sk
+
+// Non-temporal direct-to-LDS copy (the weight rows are read once per call).
+__device__ __forceinline__ void dma16s_nt(const void *sbase, uint32_t voff, uint32_t m0_value) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt" ::"s"(m0_value), "v"(voff),
+               "s"(sbase)
+               : "memory", "m0");
+}
+
+// 16-byte buffer stores and loads at device scope (cache policy sc1): written
+// through to, and read from, the level all XCDs share, so partial sums pass
+// between workgroups on any XCD without a cache-wide fence. Buffer
+// instructions, so the compiler tracks their waits; out-of-range offsets
+// read zeros and drop stores.
+constexpr int kCpolSc1 = 16;
+constexpr int kRsrcWord3 = 0x00020000;  // raw (untyped) buffer, gfx9 family
+typedef unsigned int u32x4_sk __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store_dev16(__amdgpu_buffer_rsrc_t r, uint32_t off, const f32x4 &v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_sk, v), r, (int)off, 0, kCpolSc1);
+}
+__device__ __forceinline__ f32x4 load_dev16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kCpolSc1));
+}
+
+// Wait until at most `younger` stages of CP copies are in flight for this wave.
+template <int CP, int D>
+__device__ __forceinline__ void wait_stages(int younger) {
+  static_assert((D - 1) * CP <= 63, "vmcnt is a 6-bit counter");
+  if constexpr (D > 5) if (younger >= 5) { wait_vmcnt<5 * CP>(); return; }
+  if constexpr (D > 4) if (younger >= 4) { wait_vmcnt<4 * CP>(); return; }
+  if constexpr (D > 3) if (younger >= 3) { wait_vmcnt<3 * CP>(); return; }
+  if constexpr (D > 2) if (younger >= 2) { wait_vmcnt<2 * CP>(); return; }
+  if (younger >= 1) { wait_vmcnt<CP>(); return; }
+  wait_vmcnt<0>();
+}
+
+template <int DT, int MT, int TW, bool GU>
+__global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__ xb, int64_t ldx,
+                                                        const char *__restrict__ wb, int64_t ldw,
+                                                        const float *__restrict__ scale,
+                                                        const void *__restrict__ bias, int bias_dt,
+                                                        uint16_t *__restrict__ y, int64_t ldy, int M, int N, int K,
+                                                        int kc, int S, int NB, int spread,
+                                                        float *__restrict__ part, int *__restrict__ cnt) {
+  using A = Act<DT>;
+  using namespace sk;
+  constexpr int NTW = ntw(TW, GU);
+  constexpr int WL = 2 * NTW;  // weight copies per stage per wave
+  constexpr int CP = WL + MT;  // copies per stage per wave
+  constexpr int D = depth(MT, TW, GU);
+  constexpr int XS = x_slot(MT), WS = w_slot(TW, GU);
+  constexpr int XRING = 0, WRING = (D + 1) * XS;
+  constexpr int R = NW * TW * 16;  // output columns per unit
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes(MT, TW, GU, D)];
+  __shared__ int s_last;
+
+  // Unit -> (row block, split). Units of one row block are dealt to one XCD
+  // (hardware hands workgroup b to XCD b % 8), so the partial sums they
+  // exchange stay close; grid slots past the last row block exit at once.
+  // With `spread` (a test mode) they go to consecutive workgroups instead,
+  // i.e. to different XCDs.
+  const int b = blockIdx.x;
+  int rb, s;
+  if (spread) {
+    rb = b / S;
+    s = b % S;
+  } else {
+    const int xcd = b & 7, idx = b >> 3;
+    rb = (idx / S) * 8 + xcd;
+    s = idx % S;
+  }
+  if (rb >= NB) return;  // whole workgroup, before any barrier
+  const int n0 = rb * R;
+  const int kb = s * kc;
+  const int ke = min(K, kb + kc);
+  const int nst = (ke - kb) / KS;  // >= 1 (host)
+
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, g = lane >> 4;
+
+  // Weight copy j: wave rows 8j .. 8j+7; lane -> row 8j + lane/8, LDS slot
+  // lane%8 <- global chunk (lane%8) ^ ((row>>1)&7). Tile t of the wave: output
+  // columns n0 + 16*(wid*TW + t%TW) + i (t >= TW: the up rows N + column).
+  // Columns past N are clamped (loaded, never stored).
+  uint32_t wvoff[WL];
+#pragma unroll
+  for (int j = 0; j < WL; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    const int t = row >> 4, i = row & 15;
+    int col = n0 + 16 * (wid * TW + t % TW) + i;
+    col = col < N ? col : N - 1;
+    const int wrow = (GU && t >= TW) ? N + col : col;
+    const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+    wvoff[j] = (uint32_t)((int64_t)wrow * ldw + 16 * chunk);
+  }
+  // Activation copy c of this wave covers block rows 4i .. 4i+3, i = wid*MT + c;
+  // lane -> row 4i + lane/16, LDS slot lane%16 <- global chunk (lane%16) ^
+  // (row & 15). Rows past M read row M-1 (their columns are never stored).
+  uint32_t xvoff[MT];
+#pragma unroll
+  for (int c = 0; c < MT; ++c) {
+    const int row = 4 * (wid * MT + c) + (lane >> 4);
+    const int xrow = row < M ? row : M - 1;
+    const int chunk = (lane & 15) ^ (row & 15);
+    xvoff[c] = (uint32_t)(((int64_t)xrow * ldx + 8 * chunk) * 2);
+  }
+  const uint32_t lds0 = lds_offset(lds);
+  const uint32_t wdst = lds0 + WRING + (uint32_t)wid * WS;
+  const uint32_t xdst = lds0 + XRING + (uint32_t)(wid * MT) * 1024;
+
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    const int k = kb + st * KS;
+    const char *sw = wb + k;
+    const char *sx = xb + (int64_t)k * 2;
+    const uint32_t wd = wdst + (uint32_t)((st % D) * NW * WS);
+    const uint32_t xd = xdst + (uint32_t)((st % (D + 1)) * XS);
+#pragma unroll
+    for (int j = 0; j < WL; ++j) dma16s_nt(sw, wvoff[j], wd + 1024u * j);
+#pragma unroll
+    for (int c = 0; c < MT; ++c) dma16s<0, true>(sx, xvoff[c], xd + 1024u * c);
+  };
+
+  f32x4 acc[NTW][MT];
+#pragma unroll
+  for (int t = 0; t < NTW; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int p = 0; p < D; ++p)
+    if (p < nst) issue(p);
+
+  const int wsw = (r >> 1) & 7;  // weight-row swizzle of this lane's rows (16t + r)
+  for (int st = 0; st < nst; ++st) {
+    wait_stages<CP, D>(min(D - 1, nst - 1 - st));
+    __syncthreads();  // every wave's copies of stage st have landed
+    const uint8_t *ws = lds + WRING + ((st % D) * NW + wid) * WS;
+    const uint8_t *xs = lds + XRING + (st % (D + 1)) * XS;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint4 xf[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        xf[mt] = *reinterpret_cast<const uint4 *>(xs + (16 * mt + r) * 256 + (((4 * q + g) ^ r) << 4));
+#pragma unroll
+      for (int t = 0; t < NTW; ++t) {
+        const uint2 a8 = *reinterpret_cast<const uint2 *>(ws + (16 * t + r) * 128 +
+                                                          (((2 * q + (g >> 1)) ^ wsw) << 4) + 8 * (g & 1));
+        const uint4 a = A::dq8(a8.x, a8.y);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = A::mfma16(a, xf[mt], acc[t][mt]);
+      }
+    }
+    if (st + D < nst) {
+      // this wave's reads of weight slot st % D are done before the slot is
+      // refilled; activation slot (st + D) % (D + 1) held stage st - 1, which
+      // every wave finished before the barrier above
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue(st + D);
+    }
+  }
+
+  if (S > 1) {
+    // The partial sums are exchanged with device-scope stores and loads
+    // (sc1), which write through to / read from the level shared by all
+    // XCDs; a release / acquire fence would instead write back and
+    // invalidate the whole L2 of the XCD, a cost every unit would pay.
+    constexpr int FR = NTW * MT * 256;  // floats per wave and split
+    // this row block's partial sums: [S][NW][NTW * MT fragments][64 lanes][4]
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        part + (size_t)rb * S * NW * FR, 0, (int)(S * NW * FR * sizeof(float)), kRsrcWord3);
+    const uint32_t lo = (uint32_t)(wid * FR + lane * 4) * 4u;  // byte offset of this lane in split 0
+#pragma unroll
+    for (int t = 0; t < NTW; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        store_dev16(rs, lo + (uint32_t)(s * NW * FR + (t * MT + mt) * 256) * 4u, acc[t][mt]);
+    wait_vmcnt<0>();  // this wave's partial sums are stored
+    __syncthreads();  // and every wave's
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(&cnt[rb], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+    __syncthreads();
+    if (!s_last) return;
+    // Sum the splits in order 0..S-1 (this unit's from registers); each
+    // split's fragments are loaded together, then added.
+    f32x4 sum[NTW][MT];
+    for (int s2 = 0; s2 < S; ++s2) {
+      f32x4 v[NTW][MT];
+      if (s2 == s) {
+#pragma unroll
+        for (int t = 0; t < NTW; ++t)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) v[t][mt] = acc[t][mt];
+      } else {
+#pragma unroll
+        for (int t = 0; t < NTW; ++t)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            v[t][mt] = load_dev16(rs, lo + (uint32_t)(s2 * NW * FR + (t * MT + mt) * 256) * 4u);
+      }
+#pragma unroll
+      for (int t = 0; t < NTW; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) sum[t][mt] = s2 == 0 ? v[t][mt] : sum[t][mt] + v[t][mt];
+    }
+#pragma unroll
+    for (int t = 0; t < NTW; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[t][mt] = sum[t][mt];
+    if (threadIdx.x == 0) __hip_atomic_store(&cnt[rb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // Epilogue: lane (r, g) of tile t, m-tile mt holds columns 4g .. 4g+3 of
+  // the tile for activation row 16*mt + r.
+#pragma unroll
+  for (int t = 0; t < TW; ++t) {
+    const int nb = n0 + 16 * (wid * TW + t % TW) + 4 * g;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + r;
+      if (m >= M) continue;
+      uint16_t *yrow = y + (int64_t)m * ldy;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int n = nb + e;
+        if (n >= N) continue;
+        if (GU)
+          yrow[n] = swiglu_out<A>(acc[t][mt][e] * scale[n], acc[TW + t][mt][e] * scale[N + n]);
+        else
+          yrow[n] = A::out(epilogue_value(acc[t][mt][e], scale, bias, bias_dt, n));
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Host side.
+// ----------------------------------------------------------------------------
+namespace {
+
+int sk_mt(int64_t M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
+
+bool sk_shape_ok(int x_dt, const void *x, int64_t ldx, const int8_t *w, int64_t ldw, int64_t M, int64_t wrows,
+                 int64_t K) {
+  if (x_dt != RA_F16 && x_dt != RA_BF16) return false;
+  if (M < 1 || M > sk::kMaxM || K < sk::KS || K % sk::KS != 0 || wrows < 1) return false;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w) & 15)) return false;
+  if (ldx % 8 != 0 || ldw % 16 != 0) return false;
+  // 32-bit per-lane copy offsets (the stage's k offset is in the SGPR base)
+  if ((uint64_t)((wrows - 1) * ldw + 16 * 8) >= ((uint64_t)1 << 31)) return false;
+  if ((uint64_t)((M - 1) * ldx + 8 * 16) * 2 >= ((uint64_t)1 << 31)) return false;
+  return true;
+}
+
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
+}  // namespace
+
+// Plan: tiles per wave TW and splits S minimising the bytes the busiest CU
+// moves (one workgroup per CU: rounds x per-unit bytes), per unit
+// weight rows x kc + min(M, 16*MT) x kc x 2 activation bytes (+ the partial
+// sums written and, by one unit in S, read back when S > 1).
+SplitkPlan splitk_plan(int64_t M, int64_t N, int64_t K, bool gu, bool allow_split) {
+  SplitkPlan best{};
+  best.ok = false;
+  if (M < 1 || M > sk::kMaxM || K < sk::KS || K % sk::KS != 0 || N < 1) return best;
+  const int mt = sk_mt(M);
+  const int cus = device_cus();
+  const int64_t stages = K / sk::KS;
+  double best_t = 0;
+  for (int tw = 1; tw <= 3; ++tw) {
+    const int ntw = gu ? 2 * tw : tw;
+    const int64_t R = (int64_t)sk::NW * tw * 16;
+    const int64_t nb = (N + R - 1) / R;
+    const int smax = (allow_split && nb <= sk::kMaxCounters) ? (int)std::min<int64_t>(stages, 16) : 1;
+    for (int S = 1; S <= smax; ++S) {
+      const int64_t kst = (stages + S - 1) / S;  // stages per split
+      const int64_t se = (stages + kst - 1) / kst;
+      if (se != S) continue;                     // a split would be empty
+      const int64_t kc = kst * sk::KS;
+      const int64_t units = nb * S;
+      const int64_t slots = ((nb + 7) / 8) * 8 * S;  // grid (XCD-grouped row blocks)
+      const int64_t rounds = (units + cus - 1) / cus;
+      const double wbytes = (double)(ntw * 16 * sk::NW) * kc;
+      const double xbytes = (double)std::min<int64_t>(M, 16 * mt) * kc * 2;
+      const double pbytes = S > 1 ? (double)sk::part_floats(mt, tw, gu) * 4 * (1.0 + 1.0) : 0.0;
+      const double t = (double)rounds * (wbytes + xbytes + pbytes) + 1e-3 * (double)slots;
+      if (!best.ok || t < best_t) {
+        best = SplitkPlan{true, mt, tw, S, (int)kc, (int)nb, false, 0, 0};
+        best_t = t;
+      }
+    }
+  }
+  if (best.ok && best.S > 1) {
+    best.cnt_bytes = sk::kCounterBytes;
+    best.ws_bytes = best.cnt_bytes + (size_t)best.S * best.nb * sk::part_floats(best.mt, best.tw, gu) * 4;
+  }
+  return best;
+}
+
+namespace {
+
+template <int DT, int MT, int TW, bool GU>
+void splitk_go(const SplitkPlan &p, const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
+               const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K, void *ws,
+               hipStream_t s) {
+  const unsigned grid = (unsigned)(p.spread ? (int64_t)p.nb * p.S : ((p.nb + 7) / 8) * 8 * p.S);
+  int *cnt = static_cast<int *>(ws);
+  float *part = ws ? reinterpret_cast<float *>(static_cast<char *>(ws) + p.cnt_bytes) : nullptr;
+  hipLaunchKernelGGL((splitk_kernel<DT, MT, TW, GU>), dim3(grid), dim3(256), 0, s,
+                     static_cast<const char *>(x), ldx, reinterpret_cast<const char *>(w), ldw, scale, bias,
+                     bias_dt, static_cast<uint16_t *>(y), ldy, (int)M, (int)N, (int)K, p.kc, p.S, p.nb, p.spread ? 1 : 0,
+                     part, cnt);
+}
+
+template <int DT, bool GU>
+void splitk_dispatch(const SplitkPlan &p, const void *x, int64_t ldx, const int8_t *w, int64_t ldw,
+                     const float *scale, const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N,
+                     int64_t K, void *ws, hipStream_t s) {
+#define RA_SK(MT_, TW_)                                                                                          \
+  if (p.mt == MT_ && p.tw == TW_)                                                                              \
+    return splitk_go<DT, MT_, TW_, GU>(p, x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, ws, s);
+  RA_SK(1, 1) RA_SK(1, 2) RA_SK(1, 3)
+  RA_SK(2, 1) RA_SK(2, 2) RA_SK(2, 3)
+  RA_SK(4, 1) RA_SK(4, 2) RA_SK(4, 3)
+#undef RA_SK
+}
+
+}  // namespace
+
+bool splitk_supported(const GemmArgs &a) { return sk_shape_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.M, a.N, a.K); }
+
+bool gateup_splitk_supported(const GateUpArgs &a) {
+  return sk_shape_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.M, 2 * a.I, a.K);
+}
+
+hipError_t splitk_launch(const GemmArgs &a, const SplitkPlan &p, void *ws, hipStream_t s) {
+  if (a.x_dt == RA_F16)
+    splitk_dispatch<RA_F16, false>(p, a.x, a.ldx, a.w, a.ldw, a.scale, a.bias, a.bias_dt, a.y, a.ldy, a.M, a.N,
+                                   a.K, ws, s);
+  else
+    splitk_dispatch<RA_BF16, false>(p, a.x, a.ldx, a.w, a.ldw, a.scale, a.bias, a.bias_dt, a.y, a.ldy, a.M, a.N,
+                                    a.K, ws, s);
+  return hipGetLastError();
+}
+
+hipError_t gateup_splitk_launch(const GateUpArgs &a, const SplitkPlan &p, void *ws, hipStream_t s) {
+  if (a.x_dt == RA_F16)
+    splitk_dispatch<RA_F16, true>(p, a.x, a.ldx, a.w, a.ldw, a.scale, nullptr, RA_F32, a.h, a.ldh, a.M, a.I, a.K,
+                                  ws, s);
+  else
+    splitk_dispatch<RA_BF16, true>(p, a.x, a.ldx, a.w, a.ldw, a.scale, nullptr, RA_F32, a.h, a.ldh, a.M, a.I,
+                                   a.K, ws, s);
+  return hipGetLastError();
+}
+
+}  // namespace ra

@@ -243,37 +243,6 @@ __global__ __launch_bounds__(256, 2) void tiled_kernel(const uint16_t *__restric
 // uses its 8-byte half h, and A supplies the same k's (8-half chunk
 // 4p + 2g + h), so the B read is shared by two MFMA sub-steps.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t lds_offset(const void *p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-
-// 16 bytes per lane from global memory to LDS at M0 + OFS + 16 * lane; the
-// instruction offset OFS is added to both the global and the LDS address, so
-// up to four consecutive 1 KB copies share one M0 value (the caller passes
-// g - OFS). NEW_M0 first writes M0; an LDS DMA that reads M0 needs one wait
-// state after that SALU write.
-template <int OFS, bool NEW_M0>
-__device__ __forceinline__ void dma16(const void *g_minus_ofs, uint32_t m0_value) {
-  if (NEW_M0)
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off offset:%2" ::"s"(m0_value),
-                 "v"(g_minus_ofs), "n"(OFS)
-                 : "memory", "m0");
-  else
-    asm volatile("global_load_lds_dwordx4 %0, off offset:%1" ::"v"(g_minus_ofs), "n"(OFS) : "memory");
-}
-
-// As dma16 with the uniform part of the global address in an SGPR pair and a
-// 32-bit per-lane byte offset, so a copy needs no per-lane address arithmetic.
-template <int OFS, bool NEW_M0>
-__device__ __forceinline__ void dma16s(const void *sbase, uint32_t voff, uint32_t m0_value) {
-  if (NEW_M0)
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3" ::"s"(m0_value),
-                 "v"(voff), "s"(sbase), "n"(OFS)
-                 : "memory", "m0");
-  else
-    asm volatile("global_load_lds_dwordx4 %0, %1 offset:%2" ::"v"(voff), "s"(sbase), "n"(OFS) : "memory");
-}
-
 // Largest byte offset the 32-bit per-lane copy offsets may reach. The copy
 // bases are moved down by DMA_BIAS so that offsets minus the instruction
 // offset stay non-negative, and offsets stay below 2^31 so that they mean
@@ -304,10 +273,6 @@ struct DmaTile {
   static_assert((S - 1) * COPIES <= 63, "vmcnt is a 6-bit counter");
 };
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 
 // Wait until at most `younger` K tiles of copies (COPIES loads each) are
 // still in flight for this wave; younger <= S - 1 <= 3.

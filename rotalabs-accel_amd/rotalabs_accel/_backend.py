@@ -20,12 +20,13 @@ _lock = threading.Lock()
 _lib = None
 _load_error: str | None = None
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # enum ra_dtype
 F16, BF16, F32 = 0, 1, 2
 # enum ra_variant
-VARIANT_AUTO, VARIANT_SKINNY, VARIANT_TILED, VARIANT_GENERIC, VARIANT_GEMV, VARIANT_ROWS, VARIANT_BATCH = range(7)
+(VARIANT_AUTO, VARIANT_SKINNY, VARIANT_TILED, VARIANT_GENERIC, VARIANT_GEMV, VARIANT_ROWS, VARIANT_BATCH,
+ VARIANT_SPLITK, VARIANT_SPLITK_SPREAD) = range(9)
 
 _DTYPE_CODE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
 
@@ -35,12 +36,16 @@ def lib_path() -> str:
 
 
 def _declare(lib: ctypes.CDLL) -> None:
-    p, i32, i64, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+    p, i32, i64, f32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
     sig = {
         "ra_abi_version": ([], i32),
         "ra_strerror": ([i32], ctypes.c_char_p),
         "ra_w8a16_gemm": ([p, i64, i32, p, i64, p, p, i32, p, i64, i64, i64, i64, p], i32),
-        "ra_w8a16_gemm_ex": ([p, i64, i32, p, i64, p, p, i32, p, i64, i64, i64, i64, i32, p], i32),
+        "ra_w8a16_gemm_ex": ([p, i64, i32, p, i64, p, p, i32, p, i64, i64, i64, i64, i32, p, sz, p], i32),
+        "ra_w8a16_gemm_ws": ([p, i64, i32, p, i64, p, p, i32, p, i64, i64, i64, i64, p, sz, p], i32),
+        "ra_w8a16_gemm_workspace_size": ([i64, i64, i64, i32], sz),
+        "ra_w8a16_gateup_swiglu_ws": ([p, i64, i32, p, i64, p, p, i64, i64, i64, i64, p, sz, p], i32),
+        "ra_w8a16_gateup_workspace_size": ([i64, i64, i64, i32], sz),
         "ra_w8a16_gemm_select": ([i64, i64, i64, i32], i32),
         "ra_w8a16_gateup_swiglu": ([p, i64, i32, p, i64, p, p, i64, i64, i64, i64, p], i32),
         "ra_rmsnorm": ([p, i64, i32, p, i32, p, i64, i32, i64, i64, f32, p], i32),
@@ -107,6 +112,33 @@ def dtype_code(dtype: torch.dtype) -> int:
 def stream_handle(device: torch.device) -> int:
     """hipStream_t of torch's current stream on ``device`` (as an integer)."""
     return torch.cuda.current_stream(device).cuda_stream
+
+
+_workspaces: dict = {}
+_WS_ROUND = 1 << 20
+
+
+def workspace(device: torch.device, nbytes: int):
+    """(pointer, bytes) of a zero-filled device workspace of at least
+    ``nbytes`` for launches on torch's current stream of ``device``, or
+    (None, 0) when ``nbytes`` is 0.
+
+    The kernels that use a workspace leave it as they found it (their
+    counters back at zero), so one buffer serves every call issued on a
+    stream; each stream gets its own, as calls on different streams may
+    overlap. The buffer comes from torch's allocator (also during graph
+    capture, where its zero fill is recorded as a kernel) and grows in 1 MiB
+    steps when a larger problem needs more."""
+    if nbytes <= 0:
+        return None, 0
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, torch.cuda.current_stream(device).cuda_stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = -(-nbytes // _WS_ROUND) * _WS_ROUND
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws.data_ptr(), ws.numel()
 
 
 class on_device:

@@ -83,6 +83,20 @@ def _split_bias(bias: Optional[torch.Tensor], N: int):
     return None, bias
 
 
+_WS_SIZES: dict = {}
+
+
+def _workspace_size(lib, M: int, N: int, K: int, xdt: int, gateup: bool = False) -> int:
+    """Workspace bytes of ra_w8a16_gemm_ws / ra_w8a16_gateup_swiglu_ws for
+    this problem (cached per shape)."""
+    key = (M, N, K, xdt, gateup)
+    n = _WS_SIZES.get(key)
+    if n is None:
+        fn = lib.ra_w8a16_gateup_workspace_size if gateup else lib.ra_w8a16_gemm_workspace_size
+        n = _WS_SIZES[key] = int(fn(M, N, K, xdt))
+    return n
+
+
 def _int8_gemm_hip(x: torch.Tensor, weight_int8: torch.Tensor, scale: torch.Tensor,
                    bias: Optional[torch.Tensor], variant: int = _backend.VARIANT_AUTO) -> torch.Tensor:
     lib = _backend.load()
@@ -100,9 +114,10 @@ def _int8_gemm_hip(x: torch.Tensor, weight_int8: torch.Tensor, scale: torch.Tens
     b_ptr, b_dt = (None, _backend.F32) if b is None else (b.data_ptr(), _backend.dtype_code(b.dtype))
     y = torch.empty((M, N), dtype=x.dtype, device=dev)
     with _backend.on_device(dev):
+        ws, ws_bytes = _backend.workspace(dev, _workspace_size(lib, M, N, K, xdt))
         code = lib.ra_w8a16_gemm_ex(
             x2.data_ptr(), ldx, xdt, w.data_ptr(), ldw, s.data_ptr(), b_ptr, b_dt,
-            y.data_ptr(), N, M, N, K, variant, _backend.stream_handle(dev))
+            y.data_ptr(), N, M, N, K, variant, ws, ws_bytes, _backend.stream_handle(dev))
     _backend.check(code)
     if post_bias is not None:
         y.add_(post_bias)

@@ -25,7 +25,7 @@ import torch
 
 from rotalabs_accel import _backend
 from rotalabs_accel.kernels.activations import SwiGLU, swiglu_fused, swiglu_torch
-from rotalabs_accel.kernels.gemm import _rows, int8_gemm, int8_gemm_torch
+from rotalabs_accel.kernels.gemm import _rows, _workspace_size, int8_gemm, int8_gemm_torch
 from rotalabs_accel.kernels.normalization import rmsnorm, rmsnorm_residual_fused
 from rotalabs_accel.quantization.symmetric import quantize_weight_per_channel
 
@@ -55,10 +55,12 @@ def int8_gateup_swiglu(x: torch.Tensor, weight_gate_up: torch.Tensor, scale_gate
     s = scale_gate_up.float().contiguous()
     M = x2.shape[0]
     h = torch.empty((M, inter), dtype=x.dtype, device=dev)
+    xdt = _backend.dtype_code(x.dtype)
     with _backend.on_device(dev):
-        _backend.check(lib.ra_w8a16_gateup_swiglu(
-            x2.data_ptr(), ldx, _backend.dtype_code(x.dtype), w.data_ptr(), ldw, s.data_ptr(),
-            h.data_ptr(), inter, M, inter, K, _backend.stream_handle(dev)))
+        ws, ws_bytes = _backend.workspace(dev, _workspace_size(lib, M, inter, K, xdt, gateup=True))
+        _backend.check(lib.ra_w8a16_gateup_swiglu_ws(
+            x2.data_ptr(), ldx, xdt, w.data_ptr(), ldw, s.data_ptr(),
+            h.data_ptr(), inter, M, inter, K, ws, ws_bytes, _backend.stream_handle(dev)))
     return h.view(*x.shape[:-1], inter)
 
 

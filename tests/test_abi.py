@@ -33,7 +33,7 @@ def test_abi_version_matches_header():
 
 def test_strerror_all_codes():
     lib = _backend.load()
-    for code in range(0, 7):
+    for code in range(0, 8):
         assert lib.ra_strerror(code)
 
 
@@ -56,7 +56,15 @@ def test_argument_checks_without_device_work():
     # unknown forced variant
     buf = ctypes.create_string_buffer(64)
     p = ctypes.addressof(buf)
-    assert lib.ra_w8a16_gemm_ex(p, 16, 0, p, 16, p, n, 0, p, 16, 1, 16, 16, 99, n) == 1
+    assert lib.ra_w8a16_gemm_ex(p, 16, 0, p, 16, p, n, 0, p, 16, 1, 16, 16, 99, n, 0, n) == 1
+    # a workspace smaller than the problem needs (the split-K plan of M=17 K=28672 N=8192): refused
+    # before any launch
+    need = lib.ra_w8a16_gemm_workspace_size(17, 8192, 28672, 0)
+    assert need > 0
+    assert lib.ra_w8a16_gemm_ws(p, 28672, 0, p, 28672, p, n, 0, p, 8192, 17, 8192, 28672, p, need - 1, n) == 6
+    assert lib.ra_w8a16_gemm_workspace_size(1, 11008, 4096, 0) == 0      # row GEMV: none
+    assert lib.ra_w8a16_gemm_workspace_size(2048, 11008, 4096, 0) == 0   # tiled: none
+    assert lib.ra_w8a16_gateup_swiglu_ws(n, 0, 0, n, 0, n, n, 0, 0, 8, 8, n, 0, n) == 0
 
 
 @pytest.mark.parametrize("M,expect", [(1, 5), (2, 5), (3, 6), (4, 6), (5, 6), (16, 6), (64, 6), (65, 2), (2048, 2)])
@@ -68,6 +76,7 @@ def test_variant_selection_fallbacks():
     lib = _backend.load()
     assert lib.ra_w8a16_gemm_select(1, 8192, 28672, 1) == 5  # row GEMV: any K
     assert lib.ra_w8a16_gemm_select(3, 8192, 8192, 1) == 6   # M = 3..64, K % 128 == 0: small-batch kernel
+    assert lib.ra_w8a16_gemm_select(17, 8192, 28672, 1) == 7  # ... with K >= 16384: split K over workgroups
     assert lib.ra_w8a16_gemm_select(4, 8192, 1040, 1) == 1   # K % 128 != 0: split-K MFMA kernel
     assert lib.ra_w8a16_gemm_select(1, 64, 50, 0) == 3     # K % 16 != 0 -> generic
     assert lib.ra_w8a16_gemm_select(1, 64, 64, 2) == 3     # fp32 activations -> generic

@@ -21,16 +21,17 @@ from workloads import DECODE_SHAPES, PREFILL_SHAPES, SMALLBATCH_SHAPES, gemm_cas
 
 pytestmark = pytest.mark.gpu
 
-SKINNY, TILED, GENERIC, GEMV, ROWS, BATCH = (_backend.VARIANT_SKINNY, _backend.VARIANT_TILED,
-                                             _backend.VARIANT_GENERIC, _backend.VARIANT_GEMV, _backend.VARIANT_ROWS,
-                                             _backend.VARIANT_BATCH)
-ALL_VARIANTS = (ROWS, GEMV, BATCH, SKINNY, TILED, GENERIC)
+SKINNY, TILED, GENERIC, GEMV, ROWS, BATCH, SPLITK = (_backend.VARIANT_SKINNY, _backend.VARIANT_TILED,
+                                                     _backend.VARIANT_GENERIC, _backend.VARIANT_GEMV,
+                                                     _backend.VARIANT_ROWS, _backend.VARIANT_BATCH,
+                                                     _backend.VARIANT_SPLITK)
+ALL_VARIANTS = (ROWS, GEMV, BATCH, SPLITK, SKINNY, TILED, GENERIC)
 
 
 def _may_refuse(v, M, K):
     """The variants that cover only part of the shape space (RA_ERR_VARIANT)."""
     return ((v == GEMV and M > 4) or (v == ROWS and M > 2) or
-            (v == BATCH and (M > 64 or K % 128 != 0)))
+            (v in (BATCH, SPLITK) and (M > 64 or K % 128 != 0)))
 
 # fp64 tolerance per output dtype: ~2 ulp relative + accumulation noise
 TOL64 = {torch.float16: (2e-3, 2e-3), torch.bfloat16: (8e-3, 8e-3), torch.float32: (1e-5, 1e-4)}
@@ -110,7 +111,7 @@ def test_exact_known_answer_wide_batch(gpu, M, K, N, dt):
     x, q, s, b, exact = _exact_case(M, K, N, dt, seed=M + K + N, dev=gpu, bias=(K % 256 == 128))
     print(f"  wide batch M={M} K={K} N={N} {dt}", flush=True)
     want = exact.to(dt)
-    for v in (_backend.VARIANT_AUTO, BATCH):
+    for v in (_backend.VARIANT_AUTO, BATCH, SPLITK):
         y = _run(x, q, s, b, v).cpu()
         assert torch.equal(y, want), f"variant {v}: {(y.double() - exact).abs().max()}"
 
@@ -158,7 +159,7 @@ def test_random_vs_oracle(gpu, M, K, N, dt):
     c = gemm_case(M, K, N, seed=M + K + N, dtype=dt, outlier_rows=True)
     g = torch.Generator().manual_seed(99)
     b = (torch.randn(N, generator=g) * 0.1).to(dt)
-    for v in (_backend.VARIANT_AUTO, ROWS, GEMV, BATCH, SKINNY, TILED):
+    for v in (_backend.VARIANT_AUTO, ROWS, GEMV, BATCH, SPLITK, SKINNY, TILED):
         y = _run(c.x.to(gpu), c.q.to(gpu), c.s.to(gpu), b.to(gpu), v)
         if y is None:
             assert _may_refuse(v, M, K)
@@ -215,6 +216,58 @@ TILE_SHAPES = [(300, 192, 4096), (576, 256, 11264), (640, 128, 16384), (832, 128
 @pytest.mark.parametrize("M,K,N", TILE_SHAPES)
 def test_tiled_tile_geometries(gpu, M, K, N, dt):
     _full_size_check(gemm_case(M, K, N, seed=M + N, device=gpu, dtype=dt), gpu)
+
+
+# Split-K small-batch shapes: many splits (long K, few rows), N tails, one
+# stage per split, every activation-tile count (M <= 16, 32, 64) and the
+# cfg-3 / cfg-5 decode shapes.
+SPLITK_SHAPES = [(3, 4096, 11008), (16, 4096, 11008), (64, 4096, 11008), (8, 8192, 256), (17, 8192, 300),
+                 (33, 1024, 1000), (64, 128, 64), (5, 28672, 8192), (20, 2048, 77), (40, 512, 3000)]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K,N", SPLITK_SHAPES)
+def test_splitk_exact_and_repeated(gpu, M, K, N, dt):
+    """The split-K small-batch kernel: exact known answers (integer sums, so
+    any split, order or indexing mistake is a mismatch), then two calls in a
+    row on different inputs against the oracle bound (a counter left
+    non-zero by the first call would leave the second's output unwritten),
+    and bitwise repeatable."""
+    lib = _backend.load()
+    ws_need = lib.ra_w8a16_gemm_workspace_size(M, N, K, _backend.dtype_code(dt))
+    print(f"  split-K M={M} K={K} N={N} {dt} workspace {ws_need} B", flush=True)
+    x, q, s, b, exact = _exact_case(M, K, N, dt, seed=M + K + N, dev=gpu, bias=(N % 2 == 0))
+    for v in (SPLITK, _backend.VARIANT_SPLITK_SPREAD):   # a row block's splits on one XCD / on several
+        y = _run(x, q, s, b, v).cpu()
+        assert torch.equal(y, exact.to(dt)), f"variant {v}: max err {(y.double() - exact).abs().max()}"
+    for seed in (1, 2):
+        c = gemm_case(M, K, N, seed=seed * 1000 + M, dtype=dt, outlier_rows=True)
+        y1 = _run(c.x.to(gpu), c.q.to(gpu), c.s.to(gpu), None, SPLITK)
+        y2 = _run(c.x.to(gpu), c.q.to(gpu), c.s.to(gpu), None, SPLITK)
+        assert torch.equal(y1, y2)
+        if K * N <= 4096 * 11008 and M * K * N <= 64 * 4096 * 11008:
+            _oracle_check(y1.cpu(), c.x, c.q, c.s)
+
+
+def test_splitk_plans_share_one_workspace(gpu):
+    """Calls with different split plans (58 row blocks x 4 splits, then 94 x
+    2, then 4 x 16) on one stream share its workspace: the counters sit in a
+    fixed region that no plan's partial sums overwrite, so every call finds
+    them at zero."""
+    for (M, K, N) in [(33, 4096, 11008), (64, 1024, 6000), (8, 8192, 256), (33, 4096, 11008)]:
+        x, q, s, b, exact = _exact_case(M, K, N, torch.float16, seed=M + K + N, dev=gpu)
+        y = _run(x, q, s, b, SPLITK).cpu()
+        assert torch.equal(y, exact.to(torch.float16)), f"M={M} K={K} N={N}"
+
+
+def test_splitk_selected_for_long_k():
+    """M = 3..64 with K >= 16384 run the split-K kernel with S > 1 (a
+    workspace): the MLP's down projection at M=17 (K=28672 N=8192)."""
+    lib = _backend.load()
+    assert lib.ra_w8a16_gemm_select(17, 8192, 28672, _backend.BF16) == SPLITK
+    assert lib.ra_w8a16_gemm_workspace_size(17, 8192, 28672, _backend.BF16) > 0
+    for M in (3, 16, 64):
+        assert lib.ra_w8a16_gemm_select(M, 11008, 4096, _backend.F16) == BATCH
 
 
 @pytest.mark.parametrize("M", [1, 16, 2048])
