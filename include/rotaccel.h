@@ -107,6 +107,23 @@ int ra_w8a16_gemm_ws(const void *x, int64_t ldx, int x_dtype,
 /* Workspace bytes ra_w8a16_gemm_ws may use for this problem (0: none). */
 size_t ra_w8a16_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int x_dtype);
 
+/*
+ * ra_w8a16_gemm_ws without a caller workspace and without any allocation:
+ * the split-K kernel's workspace is a fixed 16 MiB device array of the
+ * library (one per GPU, held until the process ends), so the call allocates
+ * and frees nothing -- for callers that cannot allocate: code under HIP
+ * graph capture, serving loops and harnesses that forbid allocation. No
+ * counterpart in the reference. Same kernels and results as
+ * ra_w8a16_gemm_ws with a workspace; RA_ERR_WORKSPACE when the problem needs
+ * more than 16 MiB. Every call on a GPU shares that GPU's array: calls that
+ * may overlap on one GPU (several streams) race.
+ */
+int ra_w8a16_gemm_noalloc(const void *x, int64_t ldx, int x_dtype,
+                          const int8_t *w, int64_t ldw, const float *scale,
+                          const void *bias, int bias_dtype,
+                          void *y, int64_t ldy,
+                          int64_t M, int64_t N, int64_t K, void *stream);
+
 /* ra_w8a16_gemm_ws with an explicit kernel variant (enum ra_variant); used by
  * tests to run every kernel on the same inputs. Returns RA_ERR_VARIANT if the
  * forced variant cannot handle the shape, dtype or alignment. */

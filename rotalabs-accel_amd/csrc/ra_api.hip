@@ -78,6 +78,15 @@ int check_gemm(const GemmArgs &a) {
 
 }  // namespace
 
+namespace ra {
+// Workspace bytes the automatic selection uses for this GEMM (0: none).
+size_t auto_workspace_bytes(const GemmArgs &a) {
+  if (a.M == 0 || a.N == 0 || select_variant(a, true) != RA_VARIANT_SPLITK) return 0;
+  const SplitkPlan p = splitk_plan(a.M, a.N, a.K, false, true);
+  return p.ok ? p.ws_bytes : 0;
+}
+}  // namespace ra
+
 extern "C" {
 
 #ifdef RA_TUNING

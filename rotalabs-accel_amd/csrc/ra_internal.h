@@ -75,6 +75,9 @@ hipError_t gateup_batch_launch(const GateUpArgs &a, hipStream_t s);
 // Small-batch GEMM with split K (M <= 64, K % 128 == 0): weights and
 // activations staged by direct-to-LDS copies; S > 1 needs a workspace of
 // ws_bytes (a zeroed counter block of cnt_bytes, then the partial sums).
+// Bytes of the counter block at the start of every split-K workspace (must
+// be zero before the first use; each call leaves it zero).
+constexpr size_t kSplitkCounterBytes = 4096 * sizeof(int);
 struct SplitkPlan {
   bool ok;
   int mt, tw, S, kc, nb;
@@ -86,6 +89,10 @@ bool splitk_supported(const GemmArgs &a);
 hipError_t splitk_launch(const GemmArgs &a, const SplitkPlan &p, void *ws, hipStream_t s);
 bool gateup_splitk_supported(const GateUpArgs &a);
 hipError_t gateup_splitk_launch(const GateUpArgs &a, const SplitkPlan &p, void *ws, hipStream_t s);
+
+// Workspace bytes the automatic kernel selection of ra_w8a16_gemm_ws uses
+// for this problem (0: the selected kernel needs none).
+size_t auto_workspace_bytes(const GemmArgs &a);
 
 // Decode GEMV (M <= 4, x staged in LDS, one HBM round trip per wave).
 bool gemv_supported(const GemmArgs &a);

@@ -50,8 +50,8 @@ constexpr int kMaxD = 6;
 // Counters of the split combine sit at the start of every workspace, one
 // per row block, in a fixed region (a call never writes partial sums where
 // another plan keeps a counter); plans with more row blocks do not split.
-constexpr int kMaxCounters = 4096;
-constexpr size_t kCounterBytes = kMaxCounters * sizeof(int);
+constexpr size_t kCounterBytes = kSplitkCounterBytes;
+constexpr int kMaxCounters = (int)(kCounterBytes / sizeof(int));
 
 constexpr int ntw(int tw, bool gu) { return gu ? 2 * tw : tw; }
 constexpr int x_slot(int mt) { return mt * 4096; }            // [16*MT rows][256 bytes]

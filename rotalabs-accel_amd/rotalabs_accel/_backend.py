@@ -44,6 +44,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "ra_w8a16_gemm_ex": ([p, i64, i32, p, i64, p, p, i32, p, i64, i64, i64, i64, i32, p, sz, p], i32),
         "ra_w8a16_gemm_ws": ([p, i64, i32, p, i64, p, p, i32, p, i64, i64, i64, i64, p, sz, p], i32),
         "ra_w8a16_gemm_workspace_size": ([i64, i64, i64, i32], sz),
+        "ra_w8a16_gemm_noalloc": ([p, i64, i32, p, i64, p, p, i32, p, i64, i64, i64, i64, p], i32),
         "ra_w8a16_gateup_swiglu_ws": ([p, i64, i32, p, i64, p, p, i64, i64, i64, i64, p, sz, p], i32),
         "ra_w8a16_gateup_workspace_size": ([i64, i64, i64, i32], sz),
         "ra_w8a16_gemm_select": ([i64, i64, i64, i32], i32),

@@ -65,6 +65,12 @@ def test_argument_checks_without_device_work():
     assert lib.ra_w8a16_gemm_workspace_size(1, 11008, 4096, 0) == 0      # row GEMV: none
     assert lib.ra_w8a16_gemm_workspace_size(2048, 11008, 4096, 0) == 0   # tiled: none
     assert lib.ra_w8a16_gateup_swiglu_ws(n, 0, 0, n, 0, n, n, 0, 0, 8, 8, n, 0, n) == 0
+    # the no-allocation entry point refuses a problem whose split-K workspace exceeds its
+    # 16 MiB array (M=64 K=16384 N=57344 needs ~73 MB) before any launch; argument errors as usual
+    assert lib.ra_w8a16_gemm_workspace_size(64, 57344, 16384, 0) > 16 << 20
+    assert lib.ra_w8a16_gemm_noalloc(p, 16384, 0, p, 16384, p, n, 0, p, 57344, 64, 57344, 16384, n) == 6
+    assert lib.ra_w8a16_gemm_noalloc(n, 0, 0, n, 0, n, n, 0, n, 0, -1, 4, 4, n) == 1
+    assert lib.ra_w8a16_gemm_noalloc(n, 0, 0, n, 0, n, n, 0, n, 0, 0, 4, 4, n) == 0
 
 
 @pytest.mark.parametrize("M,expect", [(1, 5), (2, 5), (3, 6), (4, 6), (5, 6), (16, 6), (64, 6), (65, 2), (2048, 2)])
