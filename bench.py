@@ -59,7 +59,8 @@ def parse():
     p.add_argument("--prefill-steps", type=int, default=300)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", choices=("all", "decode", "prefill", "mlp", "w8a8", "shapes"), default="all",
+    p.add_argument("--only", choices=("all", "decode", "prefill", "mlp", "w8a8", "shapes", "ceiling"),
+                   default="all",
                    help="run one workload only (for profiler runs)")
     p.add_argument("--no-mlp", action="store_true", help="skip the fused-MLP timing")
     p.add_argument("--no-graph", action="store_true",
@@ -373,6 +374,60 @@ def run_shapes(args, dev):
     return rows
 
 
+PROBE_LIB = os.path.join(HERE, "rotalabs-accel_amd", "rotalabs_accel", "_lib", "librotaccel_probe.so")
+
+
+def run_read_ceiling(args, dev):
+    """Single-launch floors of the M=1 decode shapes, beside the GEMM
+    (int8_gemm's kernel) on the same weight copies: a plain read of the int8
+    [N, K] weight bytes with the M=1 kernels' access pattern and grid (one
+    row per wave, every 1 KB window of the row in flight, non-temporal loads,
+    8 rows per workgroup up to N = 8192, else 4), and the same read plus the
+    GEMV's x copy into LDS and y store ("io"). Weight copies are cycled past
+    the Infinity Cache; graph replay. Returns a list of dicts."""
+    import ctypes
+    import torch
+    from workloads import gemm_bytes, gemm_case
+    lib = ctypes.CDLL(PROBE_LIB)
+    lib.rap_stream_rows.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                    ctypes.c_void_p]
+    lib.rap_stream_rows.restype = ctypes.c_int
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    rows = []
+    for (K, N, seed) in ((4096, 4096, 1), (4096, 11008, 2), (11008, 4096, 3), (4096, 44032, 4)):
+        c = gemm_case(1, K, N, seed, device=dev)
+        ncop = max(2, -(-600_000_000 // (N * K)))
+        copies = [c.q] + [c.q.clone() for _ in range(ncop - 1)]
+        wpg = 8 if N <= 8192 else 4
+        y = torch.empty((1, N), dtype=torch.float16, device=dev)
+
+        class _Read:
+            def __init__(self, io):
+                self.io = io
+
+            def run(self, n):
+                st = torch.cuda.current_stream().cuda_stream
+                for i in range(n):
+                    rc = lib.rap_stream_rows(copies[i % ncop].data_ptr(), K, N, K, wpg, self.io, c.x.data_ptr(),
+                                             y.data_ptr(), sink.data_ptr(), st)
+                    if rc:
+                        raise RuntimeError(f"rap_stream_rows failed with {rc}")
+        read_ms, _ = time_graph(_Read(0), 600, 60, per_graph=10 * ncop)
+        io_ms, _ = time_graph(_Read(1), 600, 60, per_graph=10 * ncop)
+        gemm_ms, _ = time_graph(GemmLauncher(c.x, copies, c.s, y), 600, 60, per_graph=10 * ncop)
+        rec = {"K": K, "N": N, "weight_bytes": N * K, "read_us": round(read_ms * 1e3, 2),
+               "read_GB/s": round(N * K / (read_ms * 1e-3) / 1e9, 1), "io_us": round(io_ms * 1e3, 2),
+               "gemm_us": round(gemm_ms * 1e3, 2),
+               "gemm_GB/s": round(gemm_bytes(1, K, N) / (gemm_ms * 1e-3) / 1e9, 1),
+               "gemm_over_read": round(gemm_ms / read_ms, 3), "gemm_over_io": round(gemm_ms / io_ms, 3)}
+        rows.append(rec)
+        log(f"ceiling K={K} N={N}: read {rec['read_us']} us ({rec['read_GB/s']} GB/s), read+io {rec['io_us']} us, "
+            f"GEMM {rec['gemm_us']} us ({rec['gemm_over_read']}x read, {rec['gemm_over_io']}x read+io)")
+        del copies, c
+    return rows
+
+
 def run_mlp(args, dev):
     """Fused decoder MLP block (RMSNorm -> gate/up + SwiGLU -> down, bf16,
     H=8192, I=28672) at M=1 and M=4096, random int8 weights generated on the
@@ -487,6 +542,9 @@ def main():
     shapes = None
     if args.only in ("all", "shapes"):
         shapes = run_shapes(args, dev)
+    ceiling = None
+    if args.only in ("all", "ceiling"):
+        ceiling = run_read_ceiling(args, dev)
     mlp = None
     if args.only == "mlp" or (args.only == "all" and not args.no_mlp):
         mlp = run_mlp(args, dev)
@@ -542,6 +600,12 @@ def main():
         out["shapes"] = {"workload": "the other decode (M=1) and small-batch shapes: fp16 x ~N(0,1) (1% of "
                                      "rows x20 for M > 1), int8 per-channel W from N(0,0.02), weight copies "
                                      "cycled past the Infinity Cache, HIP graph replay", "rows": shapes}
+    if ceiling is not None:
+        out["decode_read_ceiling"] = {
+            "workload": "single-launch floors of the M=1 shapes: a plain streaming read of the weights with "
+                        "the decode kernels' pattern and grid (one row per wave, all windows in flight, "
+                        "non-temporal) and the same read plus the x copy into LDS and the y store (io), beside "
+                        "the GEMM on the same copies; graph replay", "rows": ceiling}
     if w8a8 is not None:
         out["w8a8"] = w8a8
     if mlp is not None:

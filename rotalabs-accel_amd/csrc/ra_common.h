@@ -44,6 +44,21 @@ __device__ __forceinline__ uint4 load_stream16(const void *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// One 32-bit (16-bit) word through the vector memory path (a buffer load)
+// although its address is wave-uniform. The decode kernels load their
+// epilogue operands (scale, bias) this way: as scalar loads they share the
+// lgkm counter with the kernel-argument loads, and the compiler's next wait
+// for an argument (lgkmcnt(0): scalar loads return out of order) would hold
+// the row's weight loads back by one memory round trip.
+__device__ __forceinline__ uint32_t vload_b32(const void *p) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, 4, 0x00020000);
+  return __builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 0);
+}
+__device__ __forceinline__ uint32_t vload_b16(const void *p) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, 2, 0x00020000);
+  return __builtin_amdgcn_raw_buffer_load_b16(r, 0, 0, 0);
+}
+
 // ---------------------------------------------------------------------------
 // Direct-to-LDS copies (gfx950 global_load_lds_dwordx4) and explicit waits.
 // LDS byte address of a __shared__ object (what M0 and ds_* addresses use).

@@ -98,12 +98,12 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t *__restri
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
     const int n = min(n0 + r, N - 1);
-    sc[r] = scale[n];
-    su[r] = GU ? scale[N + n] : 0.f;
+    sc[r] = __uint_as_float(vload_b32(scale + n));
+    su[r] = GU ? __uint_as_float(vload_b32(scale + N + n)) : 0.f;
     bb[r] = 0;
     if (!GU && bias) {
-      if (bias_dt == RA_F32) bb[r] = static_cast<const uint32_t *>(bias)[n];
-      else bb[r] = static_cast<const uint16_t *>(bias)[n];
+      if (bias_dt == RA_F32) bb[r] = vload_b32(static_cast<const uint32_t *>(bias) + n);
+      else bb[r] = vload_b16(static_cast<const uint16_t *>(bias) + n);
     }
   }
 
@@ -214,7 +214,8 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rows_lds_kernel(const uint16_t 
                                                             // first loads must stay in front of the copy wait)
                                                             const float *__restrict__ scale,
                                                             const void *__restrict__ bias, int bias_dt,
-                                                            uint16_t *__restrict__ y, int N, int K) {
+                                                            int N, int K,  // (ahead of y: preloaded)
+                                                            uint16_t *__restrict__ y) {
   using A = Act<DT>;
   constexpr int NR = GU ? 2 * RW : RW;
   constexpr int WLOADS = kRowsCh * NR;  // weight loads of the first step
@@ -236,12 +237,12 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rows_lds_kernel(const uint16_t 
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
     const int n = min(n0 + r, N - 1);
-    sc[r] = scale[n];
-    su[r] = GU ? scale[N + n] : 0.f;
+    sc[r] = __uint_as_float(vload_b32(scale + n));
+    su[r] = GU ? __uint_as_float(vload_b32(scale + N + n)) : 0.f;
     bb[r] = 0;
     if (!GU && bias) {
-      if (bias_dt == RA_F32) bb[r] = static_cast<const uint32_t *>(bias)[n];
-      else bb[r] = static_cast<const uint16_t *>(bias)[n];
+      if (bias_dt == RA_F32) bb[r] = vload_b32(static_cast<const uint32_t *>(bias) + n);
+      else bb[r] = vload_b16(static_cast<const uint16_t *>(bias) + n);
     }
   }
   // x -> LDS: 1 KB chunks, chunk j by wave j % WPG, lane -> bytes 16 lane of
@@ -268,6 +269,9 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rows_lds_kernel(const uint16_t 
     for (int t = 0; t < NR; ++t) wv[c][t] = load_stream16(wr[t] + 1024 * c);
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(WLOADS) : "memory");  // this wave's copies have landed
   asm volatile("s_barrier" ::: "memory");                         // every wave's copies have landed
+  // Nothing that uses the first step's weights may move in front of the
+  // barrier (it would bring the wait for them along).
+  __builtin_amdgcn_sched_barrier(0);
 
   const uint16_t *xr = xl + 16 * lane;
   for (int step = 0; step < full; ++step) {
@@ -278,29 +282,17 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rows_lds_kernel(const uint16_t 
 #pragma unroll
         for (int t = 0; t < NR; ++t) wv[c][t] = load_stream16(wr[t] + k0 + 1024 * c);
     }
-    uint4 xa[kRowsCh], xb[kRowsCh];
+    // Window by window, each as soon as its weights are in: the compiler
+    // would otherwise wait for all of them first, putting every window's dot
+    // products behind the step's last load.
 #pragma unroll
     for (int c = 0; c < kRowsCh; ++c) {
-      xa[c] = *reinterpret_cast<const uint4 *>(xr + k0 + 1024 * c);
-      xb[c] = *reinterpret_cast<const uint4 *>(xr + k0 + 1024 * c + 8);
+      const uint4 xa = *reinterpret_cast<const uint4 *>(xr + k0 + 1024 * c);
+      const uint4 xb = *reinterpret_cast<const uint4 *>(xr + k0 + 1024 * c + 8);
+#pragma unroll
+      for (int t = 0; t < NR; ++t) acc[t] = dot16<DT>(wv[c][t], xa, xb, acc[t]);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (step == 0) {
-      // The first step's weights (loaded before the barrier) become opaque
-      // here: otherwise the compiler starts their dequantisation, and waits
-      // for them, in front of the barrier.
-#pragma unroll
-      for (int c = 0; c < kRowsCh; ++c)
-#pragma unroll
-        for (int t = 0; t < NR; ++t) {
-          uint32_t a0 = wv[c][t].x, a1 = wv[c][t].y, a2 = wv[c][t].z, a3 = wv[c][t].w;
-          asm volatile("" : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3)::"memory");
-          wv[c][t] = make_uint4(a0, a1, a2, a3);
-        }
-    }
-#pragma unroll
-    for (int c = 0; c < kRowsCh; ++c)
-#pragma unroll
-      for (int t = 0; t < NR; ++t) acc[t] = dot16<DT>(wv[c][t], xa[c], xb[c], acc[t]);
   }
   // Tail (fewer than kRowsCh windows left): one step with all its weight
   // loads issued before the first use; chunks past K read the row's first
@@ -341,6 +333,104 @@ __global__ __launch_bounds__(64 * WPG) void gemv_rows_lds_kernel(const uint16_t 
                                  : (bias_dt == RA_F16 ? f16_to_f32((uint16_t)bb[r]) : bf16_to_f32((uint16_t)bb[r]));
         y[n] = A::out(v);
       }
+    }
+  }
+}
+
+// M = 1 with one weight row per wave (with the gate/up pair, its gate and up
+// rows) and 4096 < K <= 1024 * CH: the wave issues the loads of its whole row
+// at once -- CH windows of 1 KB -- instead of stepping through it four
+// windows at a time, so every byte of the launch is in flight from the start
+// (K=11008 N=4096: three dependent steps before). x is staged in LDS per
+// workgroup as in gemv_rows_lds_kernel, rounded up to whole windows with
+// zeros: lanes past K read their row's first 16 weights (in bounds, finite)
+// against zero activations, so no lane needs a mask and the kernel has no
+// divergent branch (masked selects cost registers the resident waves need).
+template <int DT, bool GU, int WPG, int CH>
+__global__ __launch_bounds__(64 * WPG) void gemv_row1_kernel(const uint16_t *__restrict__ x,
+                                                        const int8_t *w, int64_t ldw,  // (not restrict: the
+                                                        // loads must stay in front of the copy wait)
+                                                        const float *__restrict__ scale,
+                                                        const void *__restrict__ bias, int bias_dt,
+                                                        int N, int K,  // (ahead of y: preloaded)
+                                                        uint16_t *__restrict__ y) {
+  using A = Act<DT>;
+  constexpr int NR = GU ? 2 : 1;
+  constexpr int WLOADS = CH * NR;  // weight loads of the wave
+  extern __shared__ __attribute__((aligned(16))) uint16_t xl[];  // 1024 * nwin elements
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = blockIdx.x * WPG + wid;
+  const int nc = min(n, N - 1);  // waves past N load row N - 1 and store nothing
+  const int nwin = (K + 1023) >> 10;  // windows holding k < K (<= CH)
+  const int8_t *wr[NR];
+#pragma unroll
+  for (int t = 0; t < NR; ++t) wr[t] = w + (int64_t)(t ? N + nc : nc) * ldw + 16 * lane;
+  // Epilogue operands first (older than the copies, so the copy wait covers them).
+  const float sc = __uint_as_float(vload_b32(scale + nc));
+  const float su = GU ? __uint_as_float(vload_b32(scale + N + nc)) : 0.f;
+  uint32_t bb = 0;
+  if (!GU && bias)
+    bb = bias_dt == RA_F32 ? vload_b32(static_cast<const uint32_t *>(bias) + nc)
+                           : vload_b16(static_cast<const uint16_t *>(bias) + nc);
+  // x -> LDS: 1 KB chunks, chunk j by wave j % WPG (as gemv_rows_lds_kernel);
+  // elements K .. 1024 nwin - 1 are zeroed (K % 16 == 0: whole 32-byte pieces).
+  const int xbytes = 2 * K;
+  const uint32_t lds0 = lds_addr(xl);
+  for (int j = wid; 1024 * j < xbytes; j += WPG) {
+    const int off = 1024 * j + 16 * lane;
+    if (off < xbytes)
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds0 + 1024 * j),
+                   "v"(reinterpret_cast<const char *>(x) + off)
+                   : "memory", "m0");
+  }
+  for (int p = (K >> 4) + (int)threadIdx.x; p < 64 * nwin; p += 64 * WPG) {
+    uint4 *q = reinterpret_cast<uint4 *>(xl + 16 * p);
+    q[0] = make_uint4(0, 0, 0, 0);
+    q[1] = make_uint4(0, 0, 0, 0);
+  }
+  // The whole row: window c holds k = 1024 c + 16 lane .. +15. Lanes whose
+  // piece starts at or past K read the row's first 16 weights instead.
+  uint4 wv[CH][NR];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int kk = 1024 * c + 16 * lane < K ? 1024 * c : -16 * lane;
+#pragma unroll
+    for (int t = 0; t < NR; ++t) wv[c][t] = load_stream16(wr[t] + kk);
+  }
+  // This wave's copies have landed (the weight loads are younger), its zero
+  // stores are done, then every wave's are.
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(WLOADS) : "memory");
+  // Nothing that uses the weights may move in front of the barrier (it would
+  // bring the wait for them along).
+  __builtin_amdgcn_sched_barrier(0);
+  const uint16_t *xr = xl + 16 * lane;
+  float acc[NR];
+#pragma unroll
+  for (int t = 0; t < NR; ++t) acc[t] = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    if (c < nwin) {  // wave-uniform
+      const uint4 xa = *reinterpret_cast<const uint4 *>(xr + 1024 * c);
+      const uint4 xb = *reinterpret_cast<const uint4 *>(xr + 1024 * c + 8);
+#pragma unroll
+      for (int t = 0; t < NR; ++t) acc[t] = dot16<DT>(wv[c][t], xa, xb, acc[t]);
+    }
+    // Window by window: hoisting every window's x reads to the barrier would
+    // hold 8 more registers per window.
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const float s0 = wave_sum_dpp(acc[0]);
+  const float s1 = GU ? wave_sum_dpp(acc[NR - 1]) : 0.f;
+  if (lane == 0 && n < N) {
+    if (GU) {
+      y[n] = swiglu_out<A>(s0 * sc, s1 * su);
+    } else {
+      float v = s0 * sc;
+      if (bias)
+        v += bias_dt == RA_F32 ? __uint_as_float(bb)
+                               : (bias_dt == RA_F16 ? f16_to_f32((uint16_t)bb) : bf16_to_f32((uint16_t)bb));
+      y[n] = A::out(v);
     }
   }
 }
@@ -397,12 +487,12 @@ __global__ __launch_bounds__(256) void gemv_rows_pipe_kernel(const uint16_t *__r
 #pragma unroll
   for (int r = 0; r < RP; ++r) {
     const int n = min(n0 + r, N - 1);
-    sc[r] = scale[n];
-    su[r] = GU ? scale[N + n] : 0.f;
+    sc[r] = __uint_as_float(vload_b32(scale + n));
+    su[r] = GU ? __uint_as_float(vload_b32(scale + N + n)) : 0.f;
     bb[r] = 0;
     if (!GU && bias) {
-      if (bias_dt == RA_F32) bb[r] = static_cast<const uint32_t *>(bias)[n];
-      else bb[r] = static_cast<const uint16_t *>(bias)[n];
+      if (bias_dt == RA_F32) bb[r] = vload_b32(static_cast<const uint32_t *>(bias) + n);
+      else bb[r] = vload_b16(static_cast<const uint16_t *>(bias) + n);
     }
   }
   // Operands of windows past K are replaced by zeros at use (selects into new
@@ -511,17 +601,43 @@ static void rows_lds_go(const RowsParams &p, hipStream_t s) {
 #endif
 #define RA_LDS_GO(WPG_)                                                                                       \
   hipLaunchKernelGGL((gemv_rows_lds_kernel<DT, RW, GU, WPG_>), dim3((unsigned)((waves + WPG_ - 1) / WPG_)),  \
-                     dim3(64 * WPG_), (size_t)2 * p.K, s, p.x, p.w, p.ldw, p.scale, p.bias, p.bias_dt, p.y, p.N, \
-                     p.K)
+                     dim3(64 * WPG_), (size_t)2 * p.K, s, p.x, p.w, p.ldw, p.scale, p.bias, p.bias_dt, p.N, p.K, \
+                     p.y)
   if (wpg == 16) RA_LDS_GO(16);
   else if (wpg == 8) RA_LDS_GO(8);
   else RA_LDS_GO(4);
 #undef RA_LDS_GO
 }
 
+// Windows per wave of gemv_row1_kernel for this K (0: not used): rows of
+// 4096 < K <= 16384 (8192 with the gate/up pair, two rows per wave).
+static int row1_windows(int64_t K, bool gu) {
+  if (K <= 4096 || K > (gu ? 8192 : 16384)) return 0;
+  const int64_t win = (K + 1023) / 1024;
+  return win <= 8 ? 8 : (win <= 12 ? 12 : 16);
+}
+
+template <int DT, bool GU, int CH>
+static void row1_go(const RowsParams &p, hipStream_t s) {
+  const int wpg = p.N <= 8192 ? 8 : 4;  // as rows_lds_go
+#define RA_ROW1_GO(WPG_)                                                                                     \
+  hipLaunchKernelGGL((gemv_row1_kernel<DT, GU, WPG_, CH>), dim3((unsigned)((p.N + WPG_ - 1) / WPG_)),       \
+                     dim3(64 * WPG_), (size_t)2048 * ((p.K + 1023) / 1024), s, p.x, p.w, p.ldw, p.scale, p.bias, p.bias_dt, p.N, p.K, \
+                     p.y)
+  if (wpg == 8) RA_ROW1_GO(8);
+  else RA_ROW1_GO(4);
+#undef RA_ROW1_GO
+}
+
 template <int DT, int MR, bool GU>
 static void rows_go_rw(const RowsParams &p, int rw, hipStream_t s) {
   if constexpr (MR == 1) {
+    const int ch = row1_windows(p.K, GU);
+    if (ch == 8) return row1_go<DT, GU, 8>(p, s);
+    if constexpr (!GU) {
+      if (ch == 12) return row1_go<DT, GU, 12>(p, s);
+      if (ch == 16) return row1_go<DT, GU, 16>(p, s);
+    }
     // x in LDS when it fits (one copy per workgroup instead of per wave) and
     // the first step is whole
     bool lds = p.K <= kRowsLdsMaxK && p.K >= 1024 * kRowsCh;

@@ -8,7 +8,13 @@ linked into rotalabs_accel/_lib/librotaccel.so. Flags that matter:
 * ``-Xclang -target-feature -Xclang -packed-fp32-ops`` keeps the compiler from
   emitting packed-fp32 VALU instructions (v_pk_{add,mul,fma}_f32);
 * ``-fhip-fp32-correctly-rounded-divide-sqrt`` and no fast-math: the weight
-  quantiser and RMSNorm depend on IEEE fp32 division / square root.
+  quantiser and RMSNorm depend on IEEE fp32 division / square root;
+* ``-mllvm -amdgpu-kernarg-preload-count=16``: the first kernel-argument
+  dwords (as many as the free user SGPRs hold, 13 for these kernels) arrive in
+  SGPRs at wave launch instead of through scalar loads. The decode kernels'
+  first weight loads wait for their arguments; each round trip of scalar
+  argument loads delays every wave's start. The argument lists put what the
+  kernels need first (pointers, sizes) ahead of the output pointer.
 """
 from __future__ import annotations
 
@@ -27,6 +33,8 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 BUILD_DIR = os.path.join(PROJ_DIR, "_build")
 LIB_DIR = os.path.join(PKG_DIR, "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "librotaccel.so")
+PROBE_SRC = os.path.join(CSRC, "probe", "ra_probe.hip")
+PROBE_LIB = os.path.join(LIB_DIR, "librotaccel_probe.so")   # bench.py --read-ceiling only
 
 ARCH = "gfx950"
 
@@ -47,6 +55,7 @@ def compile_flags() -> list[str]:
         "-fno-fast-math",
         "-fhip-fp32-correctly-rounded-divide-sqrt",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-mllvm", "-amdgpu-kernarg-preload-count=16",
         "-Wno-unused-command-line-argument",
         f"-I{INCLUDE}",
         f"-I{CSRC}",
@@ -80,6 +89,12 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH} from {len(sources)} sources")
+    # the measurement probe of bench.py (a plain streaming read; not part of the library)
+    tmp = PROBE_LIB + ".tmp"
+    res = subprocess.run([_hipcc(), *compile_flags(), "-shared", PROBE_SRC, "-o", tmp], capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {PROBE_SRC}:\n{res.stderr}")
+    os.replace(tmp, PROBE_LIB)
     return LIB_PATH
 
 
