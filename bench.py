@@ -9,7 +9,13 @@ Metric: int8_gemm HBM GB/s at M=1 and TFLOP/s at M=2048 (K=4096, N=11008).
   Steps cycle over 12 resident copies of the weight (541 MB > 2x the 256 MB
   Infinity Cache) so every step streams its weight from HBM. ``value`` =
   algorithmic bytes per step (N*K + 4N + 2MK + 2MN) / (timed region / K).
-* ``prefill``: x fp16 [2048,4096] @ W [11008,4096], TFLOP/s = 2MNK / time.
+* ``steps``: exactly ``--steps`` launches are timed (whole graphs of 120
+  launches plus one graph of the remainder).
+* ``config.python_int8_gemm_eager_us_per_call``: the Python ``int8_gemm``
+  called eagerly in a host loop at the headline shape (argument checks,
+  output allocation, C ABI call and launch), beside the graph-replay figure.
+* ``prefill``: x fp16 [2048,4096] @ W [11008,4096], TFLOP/s = 2MNK / time;
+  ``prefill_large``: the same at M=8192 K=4096 N=4096.
 * ``roofline``: the dominant kernel's achieved GB/s (TFLOP/s for prefill)
   from HIP events on the launch stream, against MI355X peaks (HBM 8 TB/s,
   dense fp16 MFMA 2516.6 TFLOP/s).
@@ -20,8 +26,8 @@ Metric: int8_gemm HBM GB/s at M=1 and TFLOP/s at M=2048 (K=4096, N=11008).
   and the small-batch shapes (M=4, 16, 64 at K=4096 N=11008), GB/s per
   call, timed like the headline.
 * ``mlp``: the fused decoder MLP block (RMSNorm -> int8 gate/up + SwiGLU ->
-  int8 down, bf16, H=8192, I=28672) per call at M=1 (GB/s) and M=4096
-  (TFLOP/s), graph replay.
+  int8 down, bf16, H=8192, I=28672) per call at M=1 and M=17 (GB/s) and
+  M=4096 (TFLOP/s), graph replay, each with its roofline.
 * ``cpu_baseline``: the reference's CPU fallback (dequantize + F.linear per
   call), restated in oracle/, timed on this host on a bounded sample.
 
@@ -44,6 +50,7 @@ PEAK_FP16_TFLOPS = 2516.6
 METRIC = "int8_gemm HBM GB/s @M=1 + TFLOP/s @M=2048 (K=4096,N=11008)"
 DECODE = (1, 4096, 11008, 2)        # M, K, N, seed
 PREFILL = (2048, 4096, 11008, 7)
+PREFILL_LARGE = (8192, 4096, 4096, 8)   # the second prefill shape of the workload set
 N_COPIES = 12
 
 
@@ -59,7 +66,8 @@ def parse():
     p.add_argument("--prefill-steps", type=int, default=300)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--only", choices=("all", "decode", "prefill", "mlp", "w8a8", "shapes", "ceiling"),
+    p.add_argument("--only", choices=("all", "decode", "prefill", "prefill_large", "mlp", "w8a8", "shapes",
+                                      "ceiling"),
                    default="all",
                    help="run one workload only (for profiler runs)")
     p.add_argument("--no-mlp", action="store_true", help="skip the fused-MLP timing")
@@ -153,35 +161,66 @@ def time_eager(launcher, steps: int, warmup: int):
 
 
 def time_graph(launcher, steps: int, warmup: int, per_graph: int, warm_seconds: float = 0.2):
-    """The same launches captured into one HIP graph of ``per_graph`` steps
-    and replayed; HIP events on the launch stream bracket the timed replays.
-    Untimed replays run for at least ``warmup`` steps and ``warm_seconds``
-    first, so that the timed region starts at steady clocks.
-    Returns (ms per step, steps actually timed)."""
+    """Exactly ``steps`` launches, timed as HIP graph replays: a graph of
+    ``per_graph`` launches replayed steps // per_graph times, then a graph of
+    the remaining steps % per_graph launches; HIP events on the launch
+    stream bracket the timed replays. Untimed replays run for at least
+    ``warmup`` launches and ``warm_seconds`` first, so that the timed region
+    starts at steady clocks. Returns (ms per step, steps timed)."""
     import torch
+    steps = max(1, steps)
+    full, rem = divmod(steps, per_graph)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         launcher.run(2)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        launcher.run(per_graph)
-    reps = max(1, -(-steps // per_graph))
+    graph = rest = None
+    if full:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            launcher.run(per_graph)
+    if rem:
+        rest = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(rest):
+            launcher.run(rem)
+    warm = graph or rest
+    warm_n = per_graph if graph is not None else rem
     t0, done = time.perf_counter(), 0
     while done < warmup or time.perf_counter() - t0 < warm_seconds:
-        graph.replay()
+        warm.replay()
         torch.cuda.synchronize()
-        done += per_graph
+        done += warm_n
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
-    for _ in range(reps):
+    for _ in range(full):
         graph.replay()
+    if rest is not None:
+        rest.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / (reps * per_graph), reps * per_graph
+    return start.elapsed_time(end) / steps, steps
+
+
+def time_python_int8_gemm(x, copies, scale, steps: int, warmup: int):
+    """The Python ``int8_gemm`` called eagerly in a host loop (argument
+    checks, output allocation, the C ABI call and its launch), cycling the
+    weight copies; HIP events on torch's current stream. ms per call."""
+    import torch
+    import rotalabs_accel as ra
+    n = len(copies)
+    for i in range(warmup):
+        ra.int8_gemm(x, copies[i % n], scale)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        ra.int8_gemm(x, copies[i % n], scale)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
 
 
 def cpu_baseline(M, K, N, seed, budget_s):
@@ -234,23 +273,26 @@ def run_decode(args, dev):
     log(f"decode M={M} K={K} N={N}: variant {variant}, {N_COPIES} weight copies "
         f"({N_COPIES * N * K / 2**20:.0f} MiB), warmup {args.warmup}, steps {args.steps}")
     ms_eager = time_eager(launcher, min(args.steps, 2000), args.warmup)
+    ms_py = time_python_int8_gemm(c.x, copies, c.s, min(args.steps, 2000), args.warmup)
     if args.no_graph:
-        ms, timed_steps = ms_eager, min(args.steps, 2000)
+        ms, timed_steps = time_eager(launcher, args.steps, args.warmup), args.steps
     else:
         ms, timed_steps = time_graph(launcher, args.steps, args.warmup, per_graph=10 * N_COPIES)
     gbs = gemm_bytes(M, K, N) / (ms * 1e-3) / 1e9
     log(f"decode: {ms * 1e3:.2f} us/step ({'host loop' if args.no_graph else 'graph replay'}), {gbs:.0f} GB/s "
-        f"({gbs / PEAK_HBM_GBS:.1%} of HBM peak); host-launched loop {ms_eager * 1e3:.2f} us/step")
-    return ms, ms_eager, gbs, timed_steps, variant
+        f"({gbs / PEAK_HBM_GBS:.1%} of HBM peak); host-launched C ABI loop {ms_eager * 1e3:.2f} us/step; "
+        f"eager Python int8_gemm {ms_py * 1e3:.2f} us/call")
+    return ms, ms_eager, ms_py, gbs, timed_steps, variant
 
 
-def run_prefill(args, dev):
-    """Prefill M=2048: returns (ms/step, TFLOP/s, variant)."""
+def run_prefill(args, dev, shape=PREFILL):
+    """Prefill (M=2048 K=4096 N=11008 by default): returns (ms/step,
+    TFLOP/s, variant)."""
     import torch
     import rotalabs_accel as ra
     from rotalabs_accel import _backend
     from workloads import gemm_case, gemm_flops
-    Mp, Kp, Np, seedp = PREFILL
+    Mp, Kp, Np, seedp = shape
     cp = gemm_case(Mp, Kp, Np, seedp, device=dev)
     yp = torch.empty((Mp, Np), dtype=torch.float16, device=dev)
     pcopies = [cp.q, cp.q.clone(), cp.q.clone()]
@@ -442,7 +484,7 @@ def run_mlp(args, dev):
     q_gu, s_gu = ra.quantize_weight_per_channel(torch.randn(2 * I, H, device=dev, generator=g) * 0.02)
     q_d, s_d = ra.quantize_weight_per_channel(torch.randn(H, I, device=dev, generator=g) * 0.02)
     out = {}
-    for M, calls in ((1, 20), (4096, 3)):
+    for M, calls in ((1, 20), (17, 20), (4096, 3)):
         x = torch.randn(M, H, device=dev, generator=g).to(torch.bfloat16)
 
         class _Step:
@@ -450,13 +492,19 @@ def run_mlp(args, dev):
                 for _ in range(n):
                     int8_mlp(x, norm_w, q_gu, s_gu, q_d, s_d)
         ms, _ = time_graph(_Step(), calls * 3, calls, per_graph=calls)
-        rec = {"us_per_call": round(ms * 1e3, 2)}
-        if M == 1:
+        rec = {"us_per_call": round(ms * 1e3, 2), "steps": calls * 3}
+        if M <= 64:   # weight-streaming (HBM-bound) sizes
             gbs = mlp_bytes(M, H, I) / (ms * 1e-3) / 1e9
-            rec.update({"GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)})
+            rec.update({"GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                     "traffic": None}})
         else:
             tf = mlp_flops(M, H, I) / (ms * 1e-3) / 1e12
-            rec.update({"TFLOP/s": round(tf, 1), "frac_mfma": round(tf / PEAK_FP16_TFLOPS, 4)})
+            rec.update({"TFLOP/s": round(tf, 1), "frac_mfma": round(tf / PEAK_FP16_TFLOPS, 4),
+                        "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_FP16_TFLOPS,
+                                     "unit": "TFLOP/s", "frac": round(tf / PEAK_FP16_TFLOPS, 4),
+                                     "traffic": None}})
         out[f"M={M}"] = rec
         log(f"mlp M={M} H={H} I={I} bf16: {rec}")
         del x
@@ -524,10 +572,10 @@ def main():
 
     # ---------------- decode M=1 (headline) ----------------
     M, K, N, seed = DECODE
-    ms = ms_eager = gbs = float("nan")
+    ms = ms_eager = ms_py = gbs = float("nan")
     timed_steps, variant = 0, None
     if args.only in ("all", "decode"):
-        ms, ms_eager, gbs, timed_steps, variant = run_decode(args, dev)
+        ms, ms_eager, ms_py, gbs, timed_steps, variant = run_decode(args, dev)
     dbytes = gemm_bytes(M, K, N)
 
     # ---------------- prefill M=2048 ----------------
@@ -536,6 +584,11 @@ def main():
     pvariant = None
     if args.only in ("all", "prefill"):
         pms, tflops, pvariant = run_prefill(args, dev)
+    Ml, Kl, Nl, _ = PREFILL_LARGE
+    lms = ltflops = float("nan")
+    lvariant = None
+    if args.only in ("all", "prefill", "prefill_large"):
+        lms, ltflops, lvariant = run_prefill(args, dev, PREFILL_LARGE)
     w8a8 = None
     if args.only in ("all", "w8a8"):
         w8a8 = run_w8a8(args, dev)
@@ -580,6 +633,9 @@ def main():
             "timing": ("host-launched loop" if args.no_graph else
                        "HIP graph of 120 launches replayed") + "; HIP events on the launch stream",
             "host_launched_us_per_step": round(ms_eager * 1e3, 3),
+            "python_int8_gemm_eager_us_per_call": round(ms_py * 1e3, 3),
+            "steps_note": "steps = launches timed, exactly --steps (whole 120-launch graphs plus one graph "
+                          "of the remainder)",
         },
         "roofline": {
             "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -594,6 +650,15 @@ def main():
                          "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
                          "traffic": measured_traffic(f"prefill M={Mp} K={Kp} N={Np}",
                                                      VARIANT_KERNELS.get(pvariant, ""))},
+        },
+        "prefill_large": {
+            "metric": f"int8_gemm TFLOP/s @M={Ml} K={Kl} N={Nl}",
+            "value": round(ltflops, 1), "unit": "TFLOP/s", "ms_per_step": lms, "steps": args.prefill_steps,
+            "kernel_variant": VARIANT_NAMES.get(lvariant, str(lvariant)),
+            "roofline": {"bound": "mfma", "achieved": round(ltflops, 1), "peak": PEAK_FP16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(ltflops / PEAK_FP16_TFLOPS, 4),
+                         "traffic": measured_traffic(f"prefill M={Ml} K={Kl} N={Nl}",
+                                                     VARIANT_KERNELS.get(lvariant, ""))},
         },
     }
     if shapes is not None:

@@ -717,12 +717,15 @@ static void launch_dma_auto(const void *x, int64_t ldx, const int8_t *w, int64_t
                             const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                             hipStream_t s, int forced) {
   DmaShape c = pick_dma_shape(M, N, GU, device_cus());
+#ifdef RA_TUNING
+  // Tuning builds only: forced tile shapes.
   if (forced == 3) c = {4, 2, 2, 0};
   if (forced == 4) c = {3, 4, 2, 0};
   if (forced == 5) c = {8, 2, 1, 0};
   if (forced == 6 && !GU) c = {4, 3, 2, 0};
-#ifdef RA_TUNING
   if (forced == 7) return launch_dma<DT, GU, 4, 4, 2>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+#else
+  (void)forced;
 #endif
   if (c.wr == 1) return launch_dma<DT, GU, 8, 2, 1>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
   if (c.bmb == 3 && c.bnb == 4)
