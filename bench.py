@@ -71,6 +71,8 @@ def parse():
                    default="all",
                    help="run one workload only (for profiler runs)")
     p.add_argument("--no-mlp", action="store_true", help="skip the fused-MLP timing")
+    p.add_argument("--shape", default="",
+                   help="with --only shapes: time this one GEMM shape M,K,N instead (for profiler runs)")
     p.add_argument("--no-graph", action="store_true",
                    help="time host-launched loops instead of HIP graph replay (for counter runs)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -390,13 +392,18 @@ CONFIG_SHAPES = (("decode", 1, 4096, 4096, 1), ("decode", 1, 11008, 4096, 3),
 
 
 def run_shapes(args, dev):
-    """Decode and small-batch shapes beside the headline: list of dicts."""
+    """Decode and small-batch shapes beside the headline (or only the one
+    --shape names): list of dicts."""
     import torch
     import rotalabs_accel as ra
     from rotalabs_accel import _backend
     from workloads import gemm_bytes, gemm_case
     rows = []
-    for group, M, K, N, seed in CONFIG_SHAPES:
+    shapes = CONFIG_SHAPES
+    if args.shape:
+        M, K, N = (int(v) for v in args.shape.split(","))
+        shapes = (("shape", M, K, N, 5),)
+    for group, M, K, N, seed in shapes:
         c = gemm_case(M, K, N, seed, device=dev, outlier_rows=M > 1)
         ncop = max(2, -(-600_000_000 // (N * K)))
         copies = [c.q] + [c.q.clone() for _ in range(ncop - 1)]
@@ -405,7 +412,10 @@ def run_shapes(args, dev):
         launcher.run(1)
         torch.cuda.synchronize()
         assert torch.equal(y, ra.int8_gemm(c.x, c.q, c.s)), "timed path differs from int8_gemm"
-        ms, _ = time_graph(launcher, 600, 60, per_graph=10 * ncop)
+        if args.no_graph:
+            ms = time_eager(launcher, 600, 60)
+        else:
+            ms, _ = time_graph(launcher, 600, 60, per_graph=10 * ncop)
         gbs = gemm_bytes(M, K, N) / (ms * 1e-3) / 1e9
         variant = _backend.load().ra_w8a16_gemm_select(M, N, K, _backend.F16)
         rec = {"group": group, "M": M, "K": K, "N": N, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
