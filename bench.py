@@ -248,6 +248,65 @@ def cpu_baseline(M, K, N, seed, budget_s):
             "gbs": gemm_bytes(M, K, N) / med / 1e9, "tflops": gemm_flops(M, K, N) / med / 1e12}
 
 
+def cpu_baseline_prefill(budget_s, rows=64):
+    """The reference's CPU fallback on a bounded sample of the prefill
+    workload: the first ``rows`` rows of x (M=2048 K=4096 N=11008), whole
+    dequantisation per call as the fallback does. TFLOP/s of the sample."""
+    import torch
+    from oracle.fallback import int8_gemm_ref
+    from workloads import gemm_case, gemm_flops
+    torch.set_num_threads(os.cpu_count() or 1)
+    Mp, Kp, Np, seedp = PREFILL
+    c = gemm_case(rows, Kp, Np, seedp)
+    int8_gemm_ref(c.x, c.q, c.s)
+    times, t_end = [], time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        int8_gemm_ref(c.x, c.q, c.s)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 100:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(gemm_flops(rows, Kp, Np) / med / 1e12, 4), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{len(times)} calls of the reference fallback on the first {rows} rows of the M={Mp} "
+                      f"K={Kp} N={Np} fp16 workload (weights dequantised per call), median "
+                      f"{med * 1e3:.1f} ms/call"}
+
+
+def cpu_baseline_mlp(budget_s):
+    """The reference composition on the CPU (oracle restatement: RMSNorm,
+    dequantise-then-matmul gate/up, SwiGLU, down) for one bf16 row of the
+    H=8192 I=28672 MLP block; GB/s of the block's bytes."""
+    import torch
+    from oracle.fallback import mlp_ref
+    from workloads import mlp_bytes
+    torch.set_num_threads(os.cpu_count() or 1)
+    H, I = MLP
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(1, H, generator=g).to(torch.bfloat16)
+    nw = (1.0 + 0.01 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    q_gu = torch.randint(-127, 128, (2 * I, H), generator=g, dtype=torch.int8)
+    s_gu = torch.rand(2 * I, generator=g) * 1e-3
+    q_d = torch.randint(-127, 128, (H, I), generator=g, dtype=torch.int8)
+    s_d = torch.rand(H, generator=g) * 1e-3
+    mlp_ref(x, nw, q_gu, s_gu, q_d, s_d)
+    times, t_end = [], time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        mlp_ref(x, nw, q_gu, s_gu, q_d, s_d)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(mlp_bytes(1, H, I) / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{len(times)} calls of the reference MLP composition (weights dequantised per call) at "
+                      f"M=1 H={H} I={I} bf16, median {med * 1e3:.1f} ms/call"}
+
+
 VARIANT_NAMES = {1: "skinny", 2: "tiled", 3: "generic", 4: "gemv", 5: "rows", 6: "batch", 7: "splitk"}
 # Kernel (symbol prefix in rocprofv3 traces) that each variant launches.
 VARIANT_KERNELS = {1: "skinny_kernel", 2: "tiled_dma_kernel", 3: "generic_kernel", 4: "gemv_kernel",
@@ -615,11 +674,16 @@ def main():
         return
 
     # ---------------- CPU baseline ----------------
-    cpu = None
+    cpu = cpu_prefill = cpu_mlp = None
     if not args.no_cpu:
         log(f"CPU baseline (reference fallback restated, {os.cpu_count()} threads, ~{args.cpu_seconds:.0f} s)")
         cpu = cpu_baseline(M, K, N, seed, args.cpu_seconds)
         log(f"CPU: {cpu['med_s'] * 1e3:.2f} ms/call, {cpu['gbs']:.2f} GB/s over {cpu['calls']} calls")
+        cpu_prefill = cpu_baseline_prefill(args.cpu_seconds)
+        log(f"CPU prefill sample: {cpu_prefill}")
+        if mlp is not None:
+            cpu_mlp = cpu_baseline_mlp(args.cpu_seconds)
+            log(f"CPU MLP: {cpu_mlp}")
 
     out = {
         "metric": METRIC,
@@ -686,6 +750,10 @@ def main():
     if mlp is not None:
         out["mlp"] = {"workload": "fused decoder MLP (RMSNorm -> int8 gate/up + SwiGLU -> int8 down), bf16, "
                                   "H=8192, I=28672, random int8 per-channel weights", **mlp}
+    if cpu_prefill is not None:
+        out["prefill"]["cpu_baseline"] = cpu_prefill
+    if cpu_mlp is not None:
+        out["mlp"]["cpu_baseline"] = cpu_mlp
     if cpu is not None:
         out["cpu_baseline"] = {
             "value": round(cpu["gbs"], 3), "unit": "GB/s", "cores": cpu["threads"], "kind": "port",
