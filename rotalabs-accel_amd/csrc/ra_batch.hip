@@ -21,6 +21,8 @@
 //    MFMA layout, in flight together with the stage's weights.
 //  * Scale (+ bias) or the gate/up SwiGLU is applied to the fp32 sums, one
 //    rounding.
+// batch_xlds_kernel (below) takes M <= 16 with 2048 <= K <= 4096: the
+// activation rows stay in LDS and the weights stream in full cache lines.
 #include "ra_common.h"
 #include "ra_internal.h"
 
@@ -190,6 +192,155 @@ __global__ __launch_bounds__(NW * 64) void batch_kernel(const uint16_t *__restri
 }
 
 // ----------------------------------------------------------------------------
+// Small batch with the activation rows resident in LDS: M <= 16,
+// K % 512 == 0, 2048 <= K <= 4096.
+//
+// batch_kernel loads the activation fragments from L2 beside every weight
+// stage, in the MFMA operand layout (16 rows x 64 bytes per load
+// instruction), and holds them in registers. Here:
+//  * the workgroup (K / 512 waves, 16*RT weight rows) first copies the M
+//    activation rows into LDS with direct-to-LDS copies, one 1 KB row
+//    segment per copy (wave w copies segment w of every row; 16-byte chunk c
+//    of row j lands at chunk c ^ (j & 15), so the 16 rows an MFMA operand
+//    read touches sit in 16 distinct bank groups);
+//  * wave w owns 16-row tile t = w % RT and k in [512 RT kp, 512 RT (kp + 1))
+//    (kp = w / RT) and streams it in 4 RT stages of 128 k, each 2 loads of
+//    8 rows x 128 contiguous bytes (full cache lines), D stages in flight
+//    (stage s + D is loaded once stage s is consumed). Loads return to a
+//    wave in issue order, so with every stage in flight at once a wave's work
+//    waits for its oldest load and piles up behind the stream (measured
+//    M=16 K=4096 N=11008: 15.3 us with all 16 stages in flight, 10.9 with 2);
+//  * transposes each stage through a 2 KB wave-private LDS slot into the
+//    MFMA layout (load h gives lane l row 8h + (l >> 3), 16-byte chunk l & 7,
+//    eight lanes per cache line; the address unit takes markedly longer when
+//    consecutive lanes hit different lines, measured 9.1 vs 8.1 us for the
+//    same 45 MB): lane (p = l & 15, g = l >> 4) reads chunks 2g and 2g + 1 of
+//    row p, k in [32g, 32g + 32) of the stage, which feed 4 MFMA sub-steps of
+//    8 k; chunks XOR-swizzled by (row >> 1) & 7 (conflict-free both ways);
+//    the activation fragment of sub-step j is k = 32g + 8j .. +7 of its row
+//    (the same permutation of k on both operands);
+//  * combines the K parts of each tile through LDS in a fixed order.
+// ----------------------------------------------------------------------------
+namespace batchx {
+constexpr int kMaxM = 16;
+constexpr int kSeg = 512;                                 // k per copy segment (1 KB of fp16)
+constexpr int kMinWaves = 4;                              // K >= 2048
+constexpr int kMaxWaves = 8;                              // K <= 4096
+constexpr int kXBytes = kMaxM * kSeg * kMaxWaves * 2;     // 128 KB of activation rows
+constexpr int kSlot = 16 * 128;                           // one stage of a wave's tile
+constexpr int kLdsBytes = kXBytes + kMaxWaves * kSlot;    // 144 KB
+}  // namespace batchx
+
+template <int DT, int RT, int D>
+__global__ __launch_bounds__(512) void batch_xlds_kernel(const uint16_t *__restrict__ x, int64_t ldx,
+                                                         const int8_t *__restrict__ w, int64_t ldw,
+                                                         const float *__restrict__ scale,
+                                                         const void *__restrict__ bias, int bias_dt, int M, int N,
+                                                         uint16_t *__restrict__ y, int64_t ldy) {
+  using A = Act<DT>;
+  constexpr int ST = 4 * RT;  // 128-k stages per wave
+  __shared__ __attribute__((aligned(1024))) uint8_t xs[batchx::kLdsBytes];
+  const int nw = (int)(blockDim.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int p = lane & 15, g = lane >> 4;
+  const int tile = wid % RT, kp = wid / RT;
+  const int n0 = blockIdx.x * (16 * RT) + 16 * tile;
+  const int k0 = kp * (batchx::kSeg * RT);
+  const int row_bytes = nw * (batchx::kSeg * 2);  // LDS bytes of one activation row (2K)
+
+  // Activation rows: segment wid of row j -> LDS j * row_bytes + 1024 wid.
+  {
+    const uint32_t base = lds_offset(xs) + (uint32_t)wid * 1024u;
+    const uint16_t *src = x + batchx::kSeg * wid + 8 * lane;
+    for (int j = 0; j < M; ++j)
+      dma16<0, true>(src + (int64_t)j * ldx + 8 * ((lane ^ (j & 15)) - lane),
+                     base + (uint32_t)(j * row_bytes));
+  }
+
+  // Weight loads, oldest first: stage s, half h covers rows
+  // n0 + 8h + (lane >> 3), bytes k0 + 128s + 16 (lane & 7) .. +15. Rows past
+  // N are clamped (loaded, never stored).
+  const int8_t *wp[2];
+  uint32_t wdst[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = 8 * h + (lane >> 3), c = lane & 7;
+    int n = n0 + r;
+    n = n < N ? n : N - 1;
+    wp[h] = w + (int64_t)n * ldw + k0 + 16 * c;
+    wdst[h] = (uint32_t)(r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+  }
+  uint8_t *const slot = xs + batchx::kXBytes + wid * batchx::kSlot;
+  const int xr_off = p * 128, xsw = (p >> 1) & 7;
+  // D stages in flight; stage s + D is loaded once stage s is consumed.
+  uint4 wr[ST][2];
+#pragma unroll
+  for (int s = 0; s < D; ++s)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) wr[s][h] = load_stream16(wp[h] + 128 * s);
+
+  // The copies are older than the 2*D weight loads: once at most 2*D loads
+  // are outstanding, this wave's copies are in LDS; the barrier makes every
+  // wave's copies visible.
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * D) : "memory");
+
+  // Activation fragments: lane (p, g) reads row min(p, M - 1) (rows past M
+  // repeat row M - 1; their output columns are never stored).
+  const int rr = p < M ? p : M - 1;
+  const uint8_t *const xrow = xs + rr * row_bytes;
+  const int sw = rr & 15;
+  const int c0 = k0 / 8 + 4 * g;  // 16-byte chunk of k0 + 32g in the row
+
+  // Two accumulators (sub-steps 0-1 and 2-3) shorten the MFMA dependency chain.
+  f32x4 acc0 = f32x4{0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+#pragma unroll
+  for (int s = 0; s < ST; ++s) {
+    // LDS executes a wave's accesses in order: the reads see these writes,
+    // and the next stage's writes cannot overtake them.
+    store16(slot + wdst[0], wr[s][0]);
+    store16(slot + wdst[1], wr[s][1]);
+    uint4 xf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      xf[j] = *reinterpret_cast<const uint4 *>(xrow + (((c0 + 16 * s + j) ^ sw) << 4));
+    const uint4 X = *reinterpret_cast<const uint4 *>(slot + xr_off + (((2 * g) ^ xsw) << 4));
+    const uint4 Y = *reinterpret_cast<const uint4 *>(slot + xr_off + (((2 * g + 1) ^ xsw) << 4));
+    acc0 = A::mfma16(A::dq8(X.x, X.y), xf[0], acc0);
+    acc1 = A::mfma16(A::dq8(Y.x, Y.y), xf[2], acc1);
+    acc0 = A::mfma16(A::dq8(X.z, X.w), xf[1], acc0);
+    acc1 = A::mfma16(A::dq8(Y.z, Y.w), xf[3], acc1);
+    if (s + D < ST) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) wr[s + D][h] = load_stream16(wp[h] + 128 * (s + D));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const f32x4 acc = acc0 + acc1;
+
+  // Combine the K parts of each tile in part order; wave `tile` (kp = 0)
+  // finishes it.
+  const int parts = nw / RT;
+  f32x4 *const red = reinterpret_cast<f32x4 *>(xs);
+  f32x4 sum = acc;
+  if (parts > 1) {
+    __syncthreads();  // every wave is done reading the activation rows
+    red[wid * 64 + lane] = acc;
+    __syncthreads();
+    if (kp != 0) return;
+    sum = red[tile * 64 + lane];
+    for (int v = 1; v < parts; ++v) sum += red[(v * RT + tile) * 64 + lane];
+  }
+  if (p >= M) return;
+  uint16_t *yrow = y + (int64_t)p * ldy;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int n = n0 + 4 * g + q;
+    if (n < N) yrow[n] = A::out(epilogue_value(sum[q], scale, bias, bias_dt, n));
+  }
+}
+
+// ----------------------------------------------------------------------------
 // Host side.
 // ----------------------------------------------------------------------------
 static bool batch_shape_ok(int x_dt, const void *x, int64_t ldx, const int8_t *w, int64_t ldw, int64_t M,
@@ -314,7 +465,65 @@ static void batch_dispatch(const void *x, int64_t ldx, const int8_t *w, int64_t 
   batch_dispatch_rt<DT, 1, GU>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
 }
 
+// batch_xlds_kernel takes M <= 16 and K = 2048 .. 4096 in steps of 512
+// (K / 512 = 4 .. 8 waves) when its workgroups fit in one round of the CUs
+// (one per CU: 144 KB of LDS). Measured on MI355X against batch_kernel
+// (us, K=4096): M=16 N=11008 10.9 vs 13.4, M=4 9.8 vs 11.5, M=16 N=4096 6.5
+// vs 8.4, M=16 N=14336 12.5 vs 19.3; with fewer waves (K < 2048) the one
+// workgroup per CU leaves the weight stream short of loads in flight (K=512:
+// 2x slower), and batch_kernel stays.
+// Tiles per workgroup: a divisor of the wave count (each tile takes an equal
+// share of the waves), the fewest whose workgroups fit in one round; 0 if
+// none does.
+static int batch_xlds_rt(const GemmArgs &a, int cus) {
+  if (a.M < 1 || a.M > batchx::kMaxM || a.K % batchx::kSeg != 0) return 0;
+  const int64_t nw = a.K / batchx::kSeg;
+  if (nw < batchx::kMinWaves || nw > batchx::kMaxWaves) return 0;
+  for (int rt = 1; rt <= 4; ++rt)
+    if (nw % rt == 0 && (a.N + 16 * rt - 1) / (16 * rt) <= cus) return rt;
+  return 0;
+}
+
+// Stages in flight per wave: two with six or more waves (two per SIMD),
+// four with fewer (measured best of 1 / 2 / 3 / 4 / all).
+template <int DT, int RT, int D>
+static void batch_xlds_launch(const GemmArgs &a, hipStream_t s) {
+  const int nw = (int)(a.K / batchx::kSeg);
+  const dim3 grid((unsigned)((a.N + 16 * RT - 1) / (16 * RT)));
+  hipLaunchKernelGGL((batch_xlds_kernel<DT, RT, D>), grid, dim3(64 * nw), 0, s, static_cast<const uint16_t *>(a.x),
+                     a.ldx, a.w, a.ldw, a.scale, a.bias, a.bias_dt, (int)a.M, (int)a.N,
+                     static_cast<uint16_t *>(a.y), a.ldy);
+}
+
+template <int DT, int RT>
+static void batch_xlds_go(const GemmArgs &a, hipStream_t s) {
+  if (a.K / batchx::kSeg >= 6)
+    batch_xlds_launch<DT, RT, 2>(a, s);
+  else
+    batch_xlds_launch<DT, RT, 4>(a, s);
+}
+
+template <int DT>
+static void batch_xlds_dispatch(const GemmArgs &a, int rt, hipStream_t s) {
+  if (rt == 1) return batch_xlds_go<DT, 1>(a, s);
+  if (rt == 2) return batch_xlds_go<DT, 2>(a, s);
+  if (rt == 3) return batch_xlds_go<DT, 3>(a, s);
+  batch_xlds_go<DT, 4>(a, s);
+}
+
 hipError_t batch_launch(const GemmArgs &a, hipStream_t s) {
+  int xrt = batch_xlds_rt(a, device_cus());
+#ifdef RA_TUNING
+  extern int g_batch_xlds;  // 1: never the LDS-resident kernel
+  if (g_batch_xlds == 1) xrt = 0;
+#endif
+  if (xrt > 0) {
+    if (a.x_dt == RA_F16)
+      batch_xlds_dispatch<RA_F16>(a, xrt, s);
+    else
+      batch_xlds_dispatch<RA_BF16>(a, xrt, s);
+    return hipGetLastError();
+  }
   if (a.x_dt == RA_F16)
     batch_dispatch<RA_F16, false>(a.x, a.ldx, a.w, a.ldw, a.scale, a.bias, a.bias_dt, a.y, a.ldy, a.M, a.N, a.K, s);
   else

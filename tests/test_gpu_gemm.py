@@ -116,6 +116,30 @@ def test_exact_known_answer_wide_batch(gpu, M, K, N, dt):
         assert torch.equal(y, want), f"variant {v}: {(y.double() - exact).abs().max()}"
 
 
+# Shapes the small-batch kernel with the activation rows resident in LDS
+# takes (M <= 16, K = 2048 .. 4096 in steps of 512, K / 512 waves shared
+# equally by the workgroup's 16-row weight tiles, at most one workgroup per
+# CU): 1, 2, 3 or 4 tiles per workgroup, 1 to 7 K parts per tile, 2 or 4
+# stages in flight, M from 1 to 16, N tails inside a tile and a half-filled
+# last tile.
+XLDS_SHAPES = [(1, 2048, 16), (2, 4096, 64), (3, 3072, 77), (5, 4096, 11008), (8, 2560, 4000), (13, 2048, 300),
+               (16, 4096, 11008), (16, 3584, 4096), (11, 2048, 8193), (16, 2048, 14000), (7, 3072, 12000),
+               (6, 4096, 6000), (16, 3072, 9000)]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K,N", XLDS_SHAPES)
+def test_exact_known_answer_xlds(gpu, M, K, N, dt):
+    x, q, s, b, exact = _exact_case(M, K, N, dt, seed=3 * M + K + N, dev=gpu, bias=(N % 2 == 0))
+    print(f"  activation-resident batch M={M} K={K} N={N} {dt}", flush=True)
+    want = exact.to(dt)
+    y = _run(x, q, s, b, BATCH).cpu()
+    assert torch.equal(y, want), f"max err {(y.double() - exact).abs().max()}"
+    # twice in a row: nothing carried over between launches
+    y2 = _run(x, q, s, b, BATCH).cpu()
+    assert torch.equal(y2, y)
+
+
 def test_exact_fp32_activations(gpu):
     x, q, s, b, exact = _exact_case(9, 200, 70, torch.float32, seed=5, dev=gpu, bias=True)
     y = _run(x, q, s, b).cpu()
