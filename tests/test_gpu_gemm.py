@@ -294,6 +294,18 @@ def test_splitk_selected_for_long_k():
         assert lib.ra_w8a16_gemm_select(M, 11008, 4096, _backend.F16) == BATCH
 
 
+def test_two_rows_take_the_activation_resident_kernel():
+    """M = 2 runs the small-batch kernel where its activation-resident form
+    applies (2048 <= K <= 4096), else the row GEMV; M = 1 the row GEMV."""
+    lib = _backend.load()
+    assert lib.ra_w8a16_gemm_select(2, 11008, 4096, _backend.F16) == BATCH
+    assert lib.ra_w8a16_gemm_select(2, 4096, 2048, _backend.BF16) == BATCH
+    assert lib.ra_w8a16_gemm_select(2, 4096, 11008, _backend.F16) == ROWS
+    assert lib.ra_w8a16_gemm_select(2, 4096, 1024, _backend.F16) == ROWS
+    assert lib.ra_w8a16_gemm_select(1, 11008, 4096, _backend.F16) == ROWS
+    assert lib.ra_w8a16_gemm_workspace_size(2, 11008, 4096, _backend.F16) == 0
+
+
 @pytest.mark.parametrize("M", [1, 16, 2048])
 def test_deterministic(gpu, M):
     c = gemm_case(M, 4096, 4096, seed=21, device=gpu)
