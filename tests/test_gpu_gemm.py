@@ -140,6 +140,28 @@ def test_exact_known_answer_xlds(gpu, M, K, N, dt):
     assert torch.equal(y2, y)
 
 
+@pytest.mark.parametrize("bdt", [torch.float16, torch.bfloat16, torch.float32])
+def test_xlds_strides_and_bias_dtypes(gpu, bdt):
+    """The activation-resident kernel with row strides on both operands
+    (ldx = K + 8, ldw = K + 48: the copies and loads address each row), a
+    bias in each dtype, and a 2-byte-misaligned activation base."""
+    M, K, N = 16, 4096, 4100
+    x, q, s, _, exact = _exact_case(M, K, N, torch.float16, seed=41, dev="cpu")
+    g = torch.Generator().manual_seed(42)
+    b = torch.randint(-8, 9, (N,), generator=g).float() * 2.0 ** -4      # exact in every bias dtype
+    want = (exact + b.double()).to(torch.float16)
+    xs = _strided_on(gpu, x, K + 8)
+    ws = _strided_on(gpu, q, K + 48)
+    y = _run(xs, ws, s.to(gpu), b.to(bdt).to(gpu), BATCH).cpu()
+    assert torch.equal(y, want), f"max err {(y.double() - exact - b.double()).abs().max()}"
+    flat = torch.zeros(M * K + 1, dtype=torch.float16, device=gpu)
+    flat[1:] = x.reshape(-1).to(gpu)
+    x_mis = flat[1:].view(M, K)
+    for v in (BATCH, _backend.VARIANT_AUTO):
+        y2 = _run(x_mis, q.to(gpu), s.to(gpu), b.to(bdt).to(gpu), v).cpu()
+        assert torch.equal(y2, want)
+
+
 def test_exact_fp32_activations(gpu):
     x, q, s, b, exact = _exact_case(9, 200, 70, torch.float32, seed=5, dev=gpu, bias=True)
     y = _run(x, q, s, b).cpu()
