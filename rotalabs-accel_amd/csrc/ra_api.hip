@@ -62,6 +62,7 @@ int select_variant(const GemmArgs &a, bool have_ws) {
   // M = 3..64: the small-batch kernel (line-wide weight loads, activations
   // read once per 48 rows) where K % 128 == 0, else the split-K MFMA kernel;
   // both measured faster than the LDS GEMV, which stays as a fallback.
+  if (tiled_small_selected(a)) return RA_VARIANT_TILED;
   if (a.M <= kSkinnyMaxM && batch_supported(a)) return RA_VARIANT_BATCH;
   if (a.M <= kSkinnyMaxM && skinny_supported(a)) return RA_VARIANT_SKINNY;
   if (gemv_supported(a)) return RA_VARIANT_GEMV;

@@ -36,6 +36,9 @@ hipError_t skinny_launch(const GemmArgs &a, const SkinnyCfg &c, hipStream_t s);
 
 // Tiled (LDS-staged MFMA) kernel for large M.
 bool tiled_supported(const GemmArgs &a);
+// Whether the automatic choice runs the tiled kernel with its 64 x 64 tile
+// (M = 33..64, at least 8192 weight rows, K % 64 == 0).
+bool tiled_small_selected(const GemmArgs &a);
 hipError_t tiled_launch(const GemmArgs &a, hipStream_t s);
 
 // Generic kernel: any shape, alignment and activation dtype.

@@ -257,7 +257,7 @@ constexpr uint64_t DMA_SPAN = (uint64_t)0x7FFFFFFF - 2 * DMA_BIAS;
 // wave row (WR = 1) every weight column is dequantised by one wave instead
 // of two, for 50 % more activation reads: 256x256 as (8,2) in 1 x 4 measured
 // 1-2 % faster than (4,4) in 2 x 2.
-template <int BMB, int BNB, int WR>
+template <int BMB, int BNB, int WR, int SMAX_SMALL = 4>
 struct DmaTile {
   static constexpr int WM = 32 * BMB, WN = 32 * BNB;  // per-wave sub-tile
   static constexpr int BM = WR * WM, BN = (4 / WR) * WN, BK = 64;
@@ -267,31 +267,35 @@ struct DmaTile {
   static constexpr int A_COPIES = A_BYTES / 4096;  // 1 KB copies per wave per K tile
   static constexpr int B_COPIES = B_BYTES / 4096;
   static constexpr int COPIES = A_COPIES + B_COPIES;
-  static constexpr int S = (160 * 1024) / STAGE < 4 ? (160 * 1024) / STAGE : 4;  // pipeline depth
+  // pipeline depth: up to 4 stages, up to SMAX for small tiles
+  static constexpr int SMAX = STAGE <= 16 * 1024 ? SMAX_SMALL : 4;
+  static constexpr int S = (160 * 1024) / STAGE < SMAX ? (160 * 1024) / STAGE : SMAX;
   static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "copies must split evenly over 4 waves");
-  static_assert(S >= 2 && S <= 4, "2 to 4 stages");
+  static_assert(S >= 2 && S <= 8, "2 to 8 stages");
   static_assert((S - 1) * COPIES <= 63, "vmcnt is a 6-bit counter");
 };
 
 
 // Wait until at most `younger` K tiles of copies (COPIES loads each) are
-// still in flight for this wave; younger <= S - 1 <= 3.
-template <int COPIES>
+// still in flight for this wave; younger <= Y = S - 1 <= 7.
+template <int COPIES, int Y>
 __device__ __forceinline__ void wait_tiles(int younger) {
-  if (younger >= 3) wait_vmcnt<3 * COPIES>();
-  else if (younger == 2) wait_vmcnt<2 * COPIES>();
-  else if (younger == 1) wait_vmcnt<COPIES>();
-  else wait_vmcnt<0>();
+  if constexpr (Y == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (younger >= Y) wait_vmcnt<Y * COPIES>();
+    else wait_tiles<COPIES, Y - 1>(younger);
+  }
 }
 
-template <int DT, bool GU, int BMB, int BNB, int WR>
+template <int DT, bool GU, int BMB, int BNB, int WR, int SM = 4>
 __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__restrict__ x, int64_t ldx,
                                                            const int8_t *__restrict__ w, int64_t ldw,
                                                            const float *__restrict__ scale,
                                                            const void *__restrict__ bias, int bias_dt,
                                                            uint16_t *__restrict__ y, int64_t ldy, int M, int N,
                                                            int K, int tiles_m, int tiles_n) {
-  using G = DmaTile<BMB, BNB, WR>;
+  using G = DmaTile<BMB, BNB, WR, SM>;
   using Ac = Act<DT>;
   constexpr int BM = G::BM, BN = G::BN, BK = G::BK, WM = G::WM, WN = G::WN, S = G::S;
   constexpr int A_COPIES = G::A_COPIES, B_COPIES = G::B_COPIES, COPIES = G::COPIES;
@@ -481,7 +485,7 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
 // half the MFMAs, needs them).
 #define RA_BOUNDARY_SUBSTEP3(kt_, st_, YOUNGER_)                                                    \
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                                \
-  wait_tiles<COPIES>(YOUNGER_);                                                                     \
+  wait_tiles<COPIES, S - 1>(YOUNGER_);                                                                     \
   asm volatile("s_barrier" ::: "memory");                                                           \
   {                                                                                                 \
     const int sn_ = ((kt_) + 1) % S;                                                                \
@@ -502,7 +506,7 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
 #pragma unroll
   for (int s = 0; s < S; ++s)
     if (s < KT) RA_ISSUE(s, s);
-  wait_tiles<COPIES>(min(KT, S) - 1);
+  wait_tiles<COPIES, S - 1>(min(KT, S) - 1);
   asm volatile("s_barrier" ::: "memory");
   RA_READ_A(0, 0, fa[0]);
   RA_READ_B(0, 0, fbr[0]);
@@ -639,6 +643,16 @@ bool tiled_supported(const GemmArgs &a) {
   return tiled_shape_ok(a.x_dt, a.x, a.ldx, a.w, a.ldw, a.ldy, a.M, a.N, a.K);
 }
 
+// M <= 64 (not gate/up): 64 x 64 tiles with a six-stage copy pipeline. For
+// M = 33..64 with at least 8192 weight rows they are ahead of the
+// small-batch kernel, whose activation tiles are padded to 64 rows (M=64
+// K=4096 N=11008: 19.7 vs 23.6 us; N=4096 level); for M <= 32 behind (M=32
+// 19.6 vs 15.3, M=17 18.6 vs 12.5): the 64 x 64 tile costs about the same
+// from M = 17 to 64.
+constexpr int64_t kSmallTileMaxM = 64;
+constexpr int64_t kSmallTileMinM = 33;
+constexpr int64_t kSmallTileMinN = 8192;
+
 // The copies address x and w through 31-bit per-lane byte offsets: a launch
 // covers at most DMA_SPAN bytes of each. Larger operands are split into row
 // chunks of x (and, without the gate/up pairing, of w), one launch each.
@@ -648,11 +662,16 @@ static bool dma_span_ok(bool gu, int64_t ldx, int64_t ldw, int64_t N, int64_t K,
   return (uint64_t)((wrows - 1) * ldw + K) <= DMA_SPAN;
 }
 
-template <int DT, bool GU, int BMB, int BNB, int WR>
+bool tiled_small_selected(const GemmArgs &a) {
+  return a.M >= kSmallTileMinM && a.M <= kSmallTileMaxM && a.N >= kSmallTileMinN && a.K > 0 &&
+         a.K % tiled::BK == 0 && tiled_supported(a) && dma_span_ok(false, a.ldx, a.ldw, a.N, a.K, 256);
+}
+
+template <int DT, bool GU, int BMB, int BNB, int WR, int SM = 4>
 static void launch_dma(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
                        const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                        hipStream_t s) {
-  using G = DmaTile<BMB, BNB, WR>;
+  using G = DmaTile<BMB, BNB, WR, SM>;
   constexpr int OUTN = GU ? G::BN / 2 : G::BN;
   // Rows of x (multiple of BM) and rows of w (multiple of OUTN) per launch.
   const int64_t mc = std::max<int64_t>(G::BM, ((int64_t)((DMA_SPAN / 2 - K) / ldx) + 1) / G::BM * G::BM);
@@ -667,7 +686,7 @@ static void launch_dma(const void *x, int64_t ldx, const int8_t *w, int64_t ldw,
       const void *bi = bias ? static_cast<const void *>(static_cast<const char *>(bias) + ns * bias_sz) : nullptr;
       const int tiles_m = (int)((Mi + G::BM - 1) / G::BM);
       const int tiles_n = (int)((Ni + OUTN - 1) / OUTN);
-      hipLaunchKernelGGL((tiled_dma_kernel<DT, GU, BMB, BNB, WR>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s,
+      hipLaunchKernelGGL((tiled_dma_kernel<DT, GU, BMB, BNB, WR, SM>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s,
                          xi, ldx, w + ns * ldw, ldw, si, bi, bias_dt, yi, ldy, (int)Mi, (int)Ni, (int)K, tiles_m,
                          tiles_n);
     }
@@ -727,6 +746,12 @@ static void launch_dma_auto(const void *x, int64_t ldx, const int8_t *w, int64_t
 #else
   (void)forced;
 #endif
+  // Up to 64 rows: 64 x 64 tiles (2 x 2 waves of one 32 x 32 block each),
+  // six K tiles of copies in flight.
+  if constexpr (!GU) {
+    if (M <= kSmallTileMaxM)
+      return launch_dma<DT, GU, 1, 1, 2, 6>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  }
   if (c.wr == 1) return launch_dma<DT, GU, 8, 2, 1>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
   if (c.bmb == 3 && c.bnb == 4)
     return launch_dma<DT, GU, 3, 4, 2>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);

@@ -73,7 +73,7 @@ def test_argument_checks_without_device_work():
     assert lib.ra_w8a16_gemm_noalloc(n, 0, 0, n, 0, n, n, 0, n, 0, 0, 4, 4, n) == 0
 
 
-@pytest.mark.parametrize("M,expect", [(1, 5), (2, 6), (3, 6), (4, 6), (5, 6), (16, 6), (64, 6), (65, 2), (2048, 2)])
+@pytest.mark.parametrize("M,expect", [(1, 5), (2, 6), (3, 6), (4, 6), (5, 6), (16, 6), (32, 6), (33, 2), (64, 2), (65, 2), (2048, 2)])
 def test_variant_selection(M, expect):
     assert _backend.load().ra_w8a16_gemm_select(M, 11008, 4096, 0) == expect
 

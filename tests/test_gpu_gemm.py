@@ -162,6 +162,24 @@ def test_xlds_strides_and_bias_dtypes(gpu, bdt):
         assert torch.equal(y2, want)
 
 
+# The tiled kernel's 64 x 64 tile (M <= 64; chosen automatically for
+# M = 33..64 with >= 8192 weight rows): M tails inside the tile, N tails,
+# short and long K, bias.
+SMALL_TILE_SHAPES = [(33, 4096, 11008), (64, 4096, 11008), (50, 2048, 8200), (64, 128, 8192), (40, 576, 9000),
+                     (17, 1024, 300), (1, 64, 64)]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K,N", SMALL_TILE_SHAPES)
+def test_exact_known_answer_small_tile(gpu, M, K, N, dt):
+    x, q, s, b, exact = _exact_case(M, K, N, dt, seed=5 * M + K + N, dev=gpu, bias=(M % 2 == 0))
+    print(f"  64x64 tiles M={M} K={K} N={N} {dt}", flush=True)
+    want = exact.to(dt)
+    for v in (TILED, _backend.VARIANT_AUTO):
+        y = _run(x, q, s, b, v).cpu()
+        assert torch.equal(y, want), f"variant {v}: {(y.double() - exact).abs().max()}"
+
+
 def test_exact_fp32_activations(gpu):
     x, q, s, b, exact = _exact_case(9, 200, 70, torch.float32, seed=5, dev=gpu, bias=True)
     y = _run(x, q, s, b).cpu()
@@ -312,8 +330,12 @@ def test_splitk_selected_for_long_k():
     lib = _backend.load()
     assert lib.ra_w8a16_gemm_select(17, 8192, 28672, _backend.BF16) == SPLITK
     assert lib.ra_w8a16_gemm_workspace_size(17, 8192, 28672, _backend.BF16) > 0
-    for M in (3, 16, 64):
+    for M in (3, 16, 32):
         assert lib.ra_w8a16_gemm_select(M, 11008, 4096, _backend.F16) == BATCH
+    # M = 33..64 with >= 8192 weight rows: the tiled kernel's 64 x 64 tile
+    for M in (33, 64):
+        assert lib.ra_w8a16_gemm_select(M, 11008, 4096, _backend.F16) == TILED
+    assert lib.ra_w8a16_gemm_select(64, 4096, 4096, _backend.F16) == BATCH
 
 
 def test_two_rows_take_the_activation_resident_kernel():
