@@ -341,6 +341,165 @@ __global__ __launch_bounds__(512) void batch_xlds_kernel(const uint16_t *__restr
 }
 
 // ----------------------------------------------------------------------------
+// Gate/up pair with the SwiGLU epilogue, small batch (M <= 16), the
+// activation rows resident in LDS one K chunk at a time (the MLP's gate/up
+// GEMM at H=8192, 2 x 28672 weight rows: K=8192 in two chunks).
+//  * Each wave owns 16 output columns: gate rows n0 .. n0+15 and up rows
+//    I + n0 .. I + n0 + 15, over the whole of K (no combine between waves);
+//    the workgroup's waves take consecutive column blocks.
+//  * K is walked in chunks of kc (a multiple of 512 dividing K, M rows x kc
+//    fp16 <= 136 KB): the workgroup copies the chunk's M activation rows into
+//    LDS with direct-to-LDS copies (1 KB row segments, 16-byte chunks
+//    XOR-swizzled by the row) between two barriers, then streams the chunk's
+//    weights.
+//  * Weights in 128-k stages, per tile 2 loads of 8 rows x 128 contiguous
+//    bytes, D stages in flight (D divides the stages of a chunk), each
+//    tile's stage transposed through the wave's 2 KB LDS slot into the
+//    16x16x32 MFMA layout (as in batch_xlds_kernel); the activation
+//    fragments of a stage are read once for both tiles.
+// Measured against batch_kernel in the MLP block (same run, H=8192
+// I=28672 bf16, gate/up us): M=16 88.0-89.9 vs 113.8-114.1, M=8 86.2 vs
+// 99.8. With two 16-row activation tiles (M = 17..32) it was level at best
+// (M=17 90.5-93.0 vs 90.2-90.6), so M > 16 stays with batch_kernel.
+// ----------------------------------------------------------------------------
+namespace gux {
+constexpr int kMaxM = 16;
+constexpr int kMaxWaves = 8;
+constexpr int kSlot = 16 * 128;
+constexpr int kXBytes = 136 * 1024;                       // activation chunk
+constexpr int kLdsBytes = kXBytes + kMaxWaves * kSlot;    // 152 KB
+}  // namespace gux
+
+template <int DT, int D>
+__global__ __launch_bounds__(64 * gux::kMaxWaves) void gateup_xlds_kernel(
+    const uint16_t *__restrict__ x, int64_t ldx, const int8_t *__restrict__ w, int64_t ldw,
+    const float *__restrict__ scale, int M, int I, int K, int kc, uint16_t *__restrict__ h, int64_t ldh) {
+  using A = Act<DT>;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[gux::kLdsBytes];
+  const int nw = (int)(blockDim.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int p = lane & 15, g = lane >> 4;
+  const int n0 = (blockIdx.x * nw + wid) * 16;
+  const int row_bytes = 2 * kc;  // LDS bytes of one activation row of a chunk
+  const int nseg = kc / 512;     // 1 KB copy segments per row and chunk
+  const int spc = kc / 128;      // stages per chunk (a multiple of D)
+  const int nst = K / 128;       // stages in all
+
+  // Weight loads: stage s of tile t (0 gate, 1 up), half hh covers rows
+  // n0 + 8hh + (lane >> 3) (+ I for up), bytes 128s + 16 (lane & 7) .. +15.
+  // Rows past I are clamped (loaded, never stored).
+  const int8_t *wp[2][2];
+  uint32_t wdst[2];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int r = 8 * hh + (lane >> 3), c = lane & 7;
+    int n = n0 + r;
+    n = n < I ? n : I - 1;
+    wp[0][hh] = w + (int64_t)n * ldw + 16 * c;
+    wp[1][hh] = w + (int64_t)(I + n) * ldw + 16 * c;
+    wdst[hh] = (uint32_t)(r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+  }
+  uint8_t *const slot = lds + gux::kXBytes + wid * gux::kSlot;
+  const int xr_off = p * 128, xsw = (p >> 1) & 7;
+
+  // Copies of activation chunk c: segment sg of row m -> LDS m * row_bytes +
+  // 1024 sg, dealt to the waves in turn.
+  auto copy_chunk = [&](int c) __attribute__((always_inline)) {
+    for (int i = wid; i < M * nseg; i += nw) {
+      const int m = i / nseg, sg = i - m * nseg;
+      dma16<0, true>(x + (int64_t)m * ldx + (int64_t)c * kc + 512 * sg + 8 * (lane ^ (m & 15)),
+                     lds_offset(lds) + (uint32_t)(m * row_bytes + 1024 * sg));
+    }
+  };
+
+  copy_chunk(0);
+  uint4 wr[D][2][2];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) wr[d][t][hh] = load_stream16(wp[t][hh] + 128 * d);
+  // The copies are older than the 4*D weight loads.
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(4 * D) : "memory");
+
+  // Activation fragments: lane (p, g) reads row min(p, M - 1) (rows past M
+  // repeat row M - 1; their outputs are never stored); sub-step j of stage s
+  // (within the chunk) is the 16-byte chunk 16s + 4g + j of the row, swizzled
+  // in its low 4 bits.
+  const int rr = p < M ? p : M - 1;
+  const uint8_t *xo[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) xo[j] = lds + rr * row_bytes + (((4 * g + j) ^ (rr & 15)) << 4);
+
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+
+  auto stage = [&](int sc, const uint4 (&wt)[2][2]) __attribute__((always_inline)) {
+    uint4 xf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xf[j] = *reinterpret_cast<const uint4 *>(xo[j] + 256 * sc);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      // LDS executes a wave's accesses in order: the reads see these writes,
+      // and the next writes cannot overtake them.
+      store16(slot + wdst[0], wt[t][0]);
+      store16(slot + wdst[1], wt[t][1]);
+      const uint4 X = *reinterpret_cast<const uint4 *>(slot + xr_off + (((2 * g) ^ xsw) << 4));
+      const uint4 Y = *reinterpret_cast<const uint4 *>(slot + xr_off + (((2 * g + 1) ^ xsw) << 4));
+      acc[t] = A::mfma16(A::dq8(X.x, X.y), xf[0], acc[t]);
+      acc[t] = A::mfma16(A::dq8(X.z, X.w), xf[1], acc[t]);
+      acc[t] = A::mfma16(A::dq8(Y.x, Y.y), xf[2], acc[t]);
+      acc[t] = A::mfma16(A::dq8(Y.z, Y.w), xf[3], acc[t]);
+    }
+  };
+
+  // Every iteration consumes D stages and loads the next D (the same loads
+  // each time, so the waits count them exactly); the last D stages follow
+  // the loop. A chunk starts at a multiple of D stages: every wave has
+  // finished reading the previous chunk (LDS reads done, barrier) before its
+  // copies are issued, and all copies have landed (wait, barrier) before the
+  // chunk is read.
+  int s0 = 0;
+  for (; s0 < nst - D; s0 += D) {
+    if (s0 > 0 && s0 % spc == 0) {
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      copy_chunk(s0 / spc);
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      stage(s0 % spc + d, wr[d]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) wr[d][t][hh] = load_stream16(wp[t][hh] + 128 * (s0 + d + D));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if (s0 > 0 && s0 % spc == 0) {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    copy_chunk(s0 / spc);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    stage(s0 % spc + d, wr[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // SwiGLU of the gate/up sums: lane (p, g) holds rows 4g + q of the tile
+  // (output columns n0 + 4g + q) for activation row p.
+  if (p >= M) return;
+  uint16_t *hrow = h + (int64_t)p * ldh;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int n = n0 + 4 * g + q;
+    if (n < I) hrow[n] = swiglu_out<A>(acc[0][q] * scale[n], acc[1][q] * scale[I + n]);
+  }
+}
+
+// ----------------------------------------------------------------------------
 // Host side.
 // ----------------------------------------------------------------------------
 static bool batch_shape_ok(int x_dt, const void *x, int64_t ldx, const int8_t *w, int64_t ldw, int64_t M,
@@ -536,7 +695,60 @@ hipError_t batch_launch(const GemmArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// gateup_xlds_kernel: M <= 16, K % 512 == 0, its 16-column blocks in one
+// round of workgroups of at most 8 waves; the K chunk is the largest multiple
+// of 512 that divides K and whose M activation rows fit in 136 KB.
+struct GuxCfg {
+  int nw = 0, kc = 0;  // waves per workgroup, k per chunk (0: not this kernel)
+};
+
+static GuxCfg gateup_xlds_cfg(const GateUpArgs &a, int cus) {
+  GuxCfg c;
+  if (a.M < 1 || a.M > gux::kMaxM || a.K < 512 || a.K % 512 != 0) return c;
+  const int64_t blocks = (a.I + 15) / 16;
+  const int64_t nw = (blocks + cus - 1) / cus;
+  if (nw > gux::kMaxWaves) return c;
+  int64_t kc = std::min<int64_t>(a.K, gux::kXBytes / (2 * a.M)) / 512 * 512;
+  while (kc >= 512 && a.K % kc != 0) kc -= 512;
+  if (kc < 512) return c;
+  c.nw = (int)std::max<int64_t>(nw, 1);
+  c.kc = (int)kc;
+  return c;
+}
+
+// Four stages in flight per wave: a stream of hundreds of MB needs more than
+// the two that suit the 45 MB launches of batch_xlds_kernel (M=17 H=8192
+// I=28672, same run: 91.9 / 88.1 / 87.4 us with 2 / 4 / 8; batch_kernel
+// 91.2; M=16 89.3 / 85.1 / 84.6 against 118.3).
+template <int DT, int D = 4>
+static void gateup_xlds_launch(const GateUpArgs &a, GuxCfg c, hipStream_t s) {
+#ifdef RA_TUNING
+  extern int g_batch_xd;  // forced stages in flight
+  if constexpr (D == 4) {
+    if (g_batch_xd == 2) return gateup_xlds_launch<DT, 2>(a, c, s);
+    if (g_batch_xd == 8 && (c.kc / 128) % 8 == 0) return gateup_xlds_launch<DT, 8>(a, c, s);
+  }
+#endif
+  const int64_t blocks = (a.I + 15) / 16;
+  const dim3 grid((unsigned)((blocks + c.nw - 1) / c.nw));
+  hipLaunchKernelGGL((gateup_xlds_kernel<DT, D>), grid, dim3(64 * c.nw), 0, s,
+                     static_cast<const uint16_t *>(a.x), a.ldx, a.w, a.ldw, a.scale, (int)a.M, (int)a.I, (int)a.K,
+                     c.kc, static_cast<uint16_t *>(a.h), a.ldh);
+}
+
 hipError_t gateup_batch_launch(const GateUpArgs &a, hipStream_t s) {
+  GuxCfg gc = gateup_xlds_cfg(a, device_cus());
+#ifdef RA_TUNING
+  extern int g_batch_xlds;  // 1: never the LDS-resident kernels
+  if (g_batch_xlds == 1) gc.nw = 0;
+#endif
+  if (gc.nw > 0) {
+    if (a.x_dt == RA_F16)
+      gateup_xlds_launch<RA_F16>(a, gc, s);
+    else
+      gateup_xlds_launch<RA_BF16>(a, gc, s);
+    return hipGetLastError();
+  }
   if (a.x_dt == RA_F16)
     batch_dispatch<RA_F16, true>(a.x, a.ldx, a.w, a.ldw, a.scale, nullptr, RA_F32, a.h, a.ldh, a.M, a.I, a.K, s);
   else
