@@ -343,35 +343,35 @@ __global__ __launch_bounds__(512) void batch_xlds_kernel(const uint16_t *__restr
 // ----------------------------------------------------------------------------
 // Gate/up pair with the SwiGLU epilogue, small batch (M <= 16), the
 // activation rows resident in LDS one K chunk at a time (the MLP's gate/up
-// GEMM at H=8192, 2 x 28672 weight rows: K=8192 in two chunks).
+// GEMM at H=8192, 2 x 28672 weight rows).
 //  * Each wave owns 16 output columns: gate rows n0 .. n0+15 and up rows
 //    I + n0 .. I + n0 + 15, over the whole of K (no combine between waves);
-//    the workgroup's waves take consecutive column blocks.
+//    the workgroup's 4 waves take consecutive column blocks.
 //  * K is walked in chunks of kc (a multiple of 512 dividing K, M rows x kc
-//    fp16 <= 136 KB): the workgroup copies the chunk's M activation rows into
-//    LDS with direct-to-LDS copies (1 KB row segments, 16-byte chunks
-//    XOR-swizzled by the row) between two barriers, then streams the chunk's
-//    weights.
+//    fp16 <= 34 KB; 1024 k at M=16): the workgroup copies the chunk's M
+//    activation rows into LDS with direct-to-LDS copies (1 KB row segments,
+//    16-byte chunks XOR-swizzled by the row) between two barriers, then
+//    streams the chunk's weights. Three workgroups share a CU (42 KB of LDS
+//    each), so the others stream while one waits for its next chunk.
 //  * Weights in 128-k stages, per tile 2 loads of 8 rows x 128 contiguous
 //    bytes, D stages in flight (D divides the stages of a chunk), each
 //    tile's stage transposed through the wave's 2 KB LDS slot into the
 //    16x16x32 MFMA layout (as in batch_xlds_kernel); the activation
 //    fragments of a stage are read once for both tiles.
-// Measured against batch_kernel in the MLP block (same run, H=8192
-// I=28672 bf16, gate/up us): M=16 88.0-89.9 vs 113.8-114.1, M=8 86.2 vs
-// 99.8. With two 16-row activation tiles (M = 17..32) it was level at best
-// (M=17 90.5-93.0 vs 90.2-90.6), so M > 16 stays with batch_kernel.
+// With two 16-row activation tiles (M = 17..32; one workgroup of 7 waves
+// per CU, 4096-k chunks) it measured level with batch_kernel at best (M=17
+// gate/up 90.5-93.0 vs 90.2-90.6 us), so M > 16 stays with batch_kernel.
 // ----------------------------------------------------------------------------
 namespace gux {
 constexpr int kMaxM = 16;
-constexpr int kMaxWaves = 8;
+constexpr int kWaves = 4;                                 // per workgroup
 constexpr int kSlot = 16 * 128;
-constexpr int kXBytes = 136 * 1024;                       // activation chunk
-constexpr int kLdsBytes = kXBytes + kMaxWaves * kSlot;    // 152 KB
+constexpr int kXBytes = 34 * 1024;                        // activation chunk
+constexpr int kLdsBytes = kXBytes + kWaves * kSlot;       // 42 KB: three workgroups per CU
 }  // namespace gux
 
 template <int DT, int D>
-__global__ __launch_bounds__(64 * gux::kMaxWaves) void gateup_xlds_kernel(
+__global__ __launch_bounds__(64 * gux::kWaves) void gateup_xlds_kernel(
     const uint16_t *__restrict__ x, int64_t ldx, const int8_t *__restrict__ w, int64_t ldw,
     const float *__restrict__ scale, int M, int I, int K, int kc, uint16_t *__restrict__ h, int64_t ldh) {
   using A = Act<DT>;
@@ -695,31 +695,29 @@ hipError_t batch_launch(const GemmArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// gateup_xlds_kernel: M <= 16, K % 512 == 0, its 16-column blocks in one
-// round of workgroups of at most 8 waves; the K chunk is the largest multiple
-// of 512 that divides K and whose M activation rows fit in 136 KB.
+// gateup_xlds_kernel: M <= 16, K % 512 == 0; workgroups of 4 waves (42 KB
+// of LDS, so three share a CU and one streams while another copies its next
+// chunk); the K chunk is the largest multiple of 512 that divides K and
+// whose M activation rows fit in 34 KB. Measured (gate/up M=16 H=8192
+// I=28672, same run): 81.0 us against 89.9 with 7 waves and 4096-k chunks
+// (one workgroup per CU), 83.0 with 2048-k chunks (two per CU); 2 or 3
+// waves per workgroup 87-94.
 struct GuxCfg {
   int nw = 0, kc = 0;  // waves per workgroup, k per chunk (0: not this kernel)
 };
 
-static GuxCfg gateup_xlds_cfg(const GateUpArgs &a, int cus) {
+static GuxCfg gateup_xlds_cfg(const GateUpArgs &a) {
   GuxCfg c;
   if (a.M < 1 || a.M > gux::kMaxM || a.K < 512 || a.K % 512 != 0) return c;
-  const int64_t blocks = (a.I + 15) / 16;
-  const int64_t nw = (blocks + cus - 1) / cus;
-  if (nw > gux::kMaxWaves) return c;
   int64_t kc = std::min<int64_t>(a.K, gux::kXBytes / (2 * a.M)) / 512 * 512;
   while (kc >= 512 && a.K % kc != 0) kc -= 512;
   if (kc < 512) return c;
-  c.nw = (int)std::max<int64_t>(nw, 1);
+  const int64_t blocks = (a.I + 15) / 16;
+  c.nw = (int)std::min<int64_t>(gux::kWaves, blocks);
   c.kc = (int)kc;
   return c;
 }
 
-// Four stages in flight per wave: a stream of hundreds of MB needs more than
-// the two that suit the 45 MB launches of batch_xlds_kernel (M=17 H=8192
-// I=28672, same run: 91.9 / 88.1 / 87.4 us with 2 / 4 / 8; batch_kernel
-// 91.2; M=16 89.3 / 85.1 / 84.6 against 118.3).
 template <int DT, int D = 4>
 static void gateup_xlds_launch(const GateUpArgs &a, GuxCfg c, hipStream_t s) {
 #ifdef RA_TUNING
@@ -737,7 +735,7 @@ static void gateup_xlds_launch(const GateUpArgs &a, GuxCfg c, hipStream_t s) {
 }
 
 hipError_t gateup_batch_launch(const GateUpArgs &a, hipStream_t s) {
-  GuxCfg gc = gateup_xlds_cfg(a, device_cus());
+  GuxCfg gc = gateup_xlds_cfg(a);
 #ifdef RA_TUNING
   extern int g_batch_xlds;  // 1: never the LDS-resident kernels
   if (g_batch_xlds == 1) gc.nw = 0;

@@ -252,7 +252,7 @@ def _swiglu_chain64(g64, u64, dt):
 # (1, 4096, 6000): the M=1 kernel with x in LDS, 8 waves per workgroup, the
 # last workgroup partly past I; (16, 8192, 3000), (13, 6144, 1000),
 # (9, 1536, 777), (5, 512, 300): the gate/up kernel with the activation rows
-# in LDS (M <= 16), in 2, 2, 1 and 1 K chunks (4096, 3072, 1536 and 512 k),
+# in LDS (M <= 16), in 8, 6, 1 and 1 K chunks (1024, 1024, 1536 and 512 k),
 # I not a multiple of 16; (17, 2048, 640) and (20, 256, 8192): the
 # small-batch kernel with two 16-row activation tiles.
 @pytest.mark.parametrize("M,K,inter", [(1, 1024, 512), (5, 512, 300), (17, 2048, 640), (64, 256, 128),
