@@ -341,7 +341,7 @@ __global__ __launch_bounds__(512) void batch_xlds_kernel(const uint16_t *__restr
 }
 
 // ----------------------------------------------------------------------------
-// Gate/up pair with the SwiGLU epilogue, small batch (M <= 16), the
+// Gate/up pair with the SwiGLU epilogue, small batch (M <= 32), the
 // activation rows resident in LDS one K chunk at a time (the MLP's gate/up
 // GEMM at H=8192, 2 x 28672 weight rows).
 //  * Each wave owns 16 output columns: gate rows n0 .. n0+15 and up rows
@@ -357,20 +357,18 @@ __global__ __launch_bounds__(512) void batch_xlds_kernel(const uint16_t *__restr
 //    bytes, D stages in flight (D divides the stages of a chunk), each
 //    tile's stage transposed through the wave's 2 KB LDS slot into the
 //    16x16x32 MFMA layout (as in batch_xlds_kernel); the activation
-//    fragments of a stage are read once for both tiles.
-// With two 16-row activation tiles (M = 17..32; one workgroup of 7 waves
-// per CU, 4096-k chunks) it measured level with batch_kernel at best (M=17
-// gate/up 90.5-93.0 vs 90.2-90.6 us), so M > 16 stays with batch_kernel.
+//    fragments of a stage (MT = 1 or 2 16-row activation tiles) are read
+//    once for both weight tiles.
 // ----------------------------------------------------------------------------
 namespace gux {
-constexpr int kMaxM = 16;
+constexpr int kMaxM = 32;                                 // two 16-row activation tiles
 constexpr int kWaves = 4;                                 // per workgroup
 constexpr int kSlot = 16 * 128;
 constexpr int kXBytes = 34 * 1024;                        // activation chunk
 constexpr int kLdsBytes = kXBytes + kWaves * kSlot;       // 42 KB: three workgroups per CU
 }  // namespace gux
 
-template <int DT, int D>
+template <int DT, int D, int MT = 1>
 __global__ __launch_bounds__(64 * gux::kWaves) void gateup_xlds_kernel(
     const uint16_t *__restrict__ x, int64_t ldx, const int8_t *__restrict__ w, int64_t ldw,
     const float *__restrict__ scale, int M, int I, int K, int kc, uint16_t *__restrict__ h, int64_t ldh) {
@@ -424,21 +422,30 @@ __global__ __launch_bounds__(64 * gux::kWaves) void gateup_xlds_kernel(
   // The copies are older than the 4*D weight loads.
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(4 * D) : "memory");
 
-  // Activation fragments: lane (p, g) reads row min(p, M - 1) (rows past M
-  // repeat row M - 1; their outputs are never stored); sub-step j of stage s
-  // (within the chunk) is the 16-byte chunk 16s + 4g + j of the row, swizzled
-  // in its low 4 bits.
-  const int rr = p < M ? p : M - 1;
-  const uint8_t *xo[4];
+  // Activation fragments: lane (p, g) of 16-row activation tile mt reads row
+  // min(16 mt + p, M - 1) (rows past M repeat row M - 1; their outputs are
+  // never stored); sub-step j of stage s (within the chunk) is the 16-byte
+  // chunk 16s + 4g + j of the row, swizzled in its low 4 bits.
+  const uint8_t *xo[MT][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) xo[j] = lds + rr * row_bytes + (((4 * g + j) ^ (rr & 15)) << 4);
+  for (int mt = 0; mt < MT; ++mt) {
+    const int rr = 16 * mt + p < M ? 16 * mt + p : M - 1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xo[mt][j] = lds + rr * row_bytes + (((4 * g + j) ^ (rr & 15)) << 4);
+  }
 
-  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  f32x4 acc[2][MT];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto stage = [&](int sc, const uint4 (&wt)[2][2]) __attribute__((always_inline)) {
-    uint4 xf[4];
+    uint4 xf[MT][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xf[j] = *reinterpret_cast<const uint4 *>(xo[j] + 256 * sc);
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xf[mt][j] = *reinterpret_cast<const uint4 *>(xo[mt][j] + 256 * sc);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       // LDS executes a wave's accesses in order: the reads see these writes,
@@ -447,10 +454,14 @@ __global__ __launch_bounds__(64 * gux::kWaves) void gateup_xlds_kernel(
       store16(slot + wdst[1], wt[t][1]);
       const uint4 X = *reinterpret_cast<const uint4 *>(slot + xr_off + (((2 * g) ^ xsw) << 4));
       const uint4 Y = *reinterpret_cast<const uint4 *>(slot + xr_off + (((2 * g + 1) ^ xsw) << 4));
-      acc[t] = A::mfma16(A::dq8(X.x, X.y), xf[0], acc[t]);
-      acc[t] = A::mfma16(A::dq8(X.z, X.w), xf[1], acc[t]);
-      acc[t] = A::mfma16(A::dq8(Y.x, Y.y), xf[2], acc[t]);
-      acc[t] = A::mfma16(A::dq8(Y.z, Y.w), xf[3], acc[t]);
+      const uint4 a0 = A::dq8(X.x, X.y), a1 = A::dq8(X.z, X.w), a2 = A::dq8(Y.x, Y.y), a3 = A::dq8(Y.z, Y.w);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc[t][mt] = A::mfma16(a0, xf[mt][0], acc[t][mt]);
+        acc[t][mt] = A::mfma16(a1, xf[mt][1], acc[t][mt]);
+        acc[t][mt] = A::mfma16(a2, xf[mt][2], acc[t][mt]);
+        acc[t][mt] = A::mfma16(a3, xf[mt][3], acc[t][mt]);
+      }
     }
   };
 
@@ -489,13 +500,17 @@ __global__ __launch_bounds__(64 * gux::kWaves) void gateup_xlds_kernel(
   }
 
   // SwiGLU of the gate/up sums: lane (p, g) holds rows 4g + q of the tile
-  // (output columns n0 + 4g + q) for activation row p.
-  if (p >= M) return;
-  uint16_t *hrow = h + (int64_t)p * ldh;
+  // (output columns n0 + 4g + q) for activation rows 16 mt + p.
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int n = n0 + 4 * g + q;
-    if (n < I) hrow[n] = swiglu_out<A>(acc[0][q] * scale[n], acc[1][q] * scale[I + n]);
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + p;
+    if (m >= M) continue;
+    uint16_t *hrow = h + (int64_t)m * ldh;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = n0 + 4 * g + q;
+      if (n < I) hrow[n] = swiglu_out<A>(acc[0][mt][q] * scale[n], acc[1][mt][q] * scale[I + n]);
+    }
   }
 }
 
@@ -695,7 +710,7 @@ hipError_t batch_launch(const GemmArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// gateup_xlds_kernel: M <= 16, K % 512 == 0; workgroups of 4 waves (42 KB
+// gateup_xlds_kernel: M <= 32, K % 512 == 0; workgroups of 4 waves (42 KB
 // of LDS, so three share a CU and one streams while another copies its next
 // chunk); the K chunk is the largest multiple of 512 that divides K and
 // whose M activation rows fit in 34 KB. Measured (gate/up M=16 H=8192
@@ -718,18 +733,18 @@ static GuxCfg gateup_xlds_cfg(const GateUpArgs &a) {
   return c;
 }
 
-template <int DT, int D = 4>
+template <int DT, int D = 4, int MT = 1>
 static void gateup_xlds_launch(const GateUpArgs &a, GuxCfg c, hipStream_t s) {
 #ifdef RA_TUNING
   extern int g_batch_xd;  // forced stages in flight
   if constexpr (D == 4) {
-    if (g_batch_xd == 2) return gateup_xlds_launch<DT, 2>(a, c, s);
-    if (g_batch_xd == 8 && (c.kc / 128) % 8 == 0) return gateup_xlds_launch<DT, 8>(a, c, s);
+    if (g_batch_xd == 2) return gateup_xlds_launch<DT, 2, MT>(a, c, s);
+    if (g_batch_xd == 8 && (c.kc / 128) % 8 == 0) return gateup_xlds_launch<DT, 8, MT>(a, c, s);
   }
 #endif
   const int64_t blocks = (a.I + 15) / 16;
   const dim3 grid((unsigned)((blocks + c.nw - 1) / c.nw));
-  hipLaunchKernelGGL((gateup_xlds_kernel<DT, D>), grid, dim3(64 * c.nw), 0, s,
+  hipLaunchKernelGGL((gateup_xlds_kernel<DT, D, MT>), grid, dim3(64 * c.nw), 0, s,
                      static_cast<const uint16_t *>(a.x), a.ldx, a.w, a.ldw, a.scale, (int)a.M, (int)a.I, (int)a.K,
                      c.kc, static_cast<uint16_t *>(a.h), a.ldh);
 }
@@ -741,10 +756,13 @@ hipError_t gateup_batch_launch(const GateUpArgs &a, hipStream_t s) {
   if (g_batch_xlds == 1) gc.nw = 0;
 #endif
   if (gc.nw > 0) {
-    if (a.x_dt == RA_F16)
-      gateup_xlds_launch<RA_F16>(a, gc, s);
-    else
-      gateup_xlds_launch<RA_BF16>(a, gc, s);
+    if (a.x_dt == RA_F16) {
+      if (a.M <= 16) gateup_xlds_launch<RA_F16, 4, 1>(a, gc, s);
+      else gateup_xlds_launch<RA_F16, 4, 2>(a, gc, s);
+    } else {
+      if (a.M <= 16) gateup_xlds_launch<RA_BF16, 4, 1>(a, gc, s);
+      else gateup_xlds_launch<RA_BF16, 4, 2>(a, gc, s);
+    }
     return hipGetLastError();
   }
   if (a.x_dt == RA_F16)

@@ -251,13 +251,15 @@ def _swiglu_chain64(g64, u64, dt):
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 # (1, 4096, 6000): the M=1 kernel with x in LDS, 8 waves per workgroup, the
 # last workgroup partly past I; (16, 8192, 3000), (13, 6144, 1000),
-# (9, 1536, 777), (5, 512, 300): the gate/up kernel with the activation rows
-# in LDS (M <= 16), in 8, 6, 1 and 1 K chunks (1024, 1024, 1536 and 512 k),
-# I not a multiple of 16; (17, 2048, 640) and (20, 256, 8192): the
-# small-batch kernel with two 16-row activation tiles.
+# (9, 1536, 777), (5, 512, 300), (17, 8192, 3000), (32, 4608, 1000),
+# (17, 2048, 640): the gate/up kernel with the activation rows in LDS, one
+# or two 16-row activation tiles, in 8, 6, 1, 1, 8, 9 and 2 K chunks (1024,
+# 1024, 1536, 512, 1024, 512 and 1024 k), I not a multiple of 16;
+# (20, 256, 8192): the small-batch kernel with two activation tiles.
 @pytest.mark.parametrize("M,K,inter", [(1, 1024, 512), (5, 512, 300), (17, 2048, 640), (64, 256, 128),
                                         (5, 512, 8192), (20, 256, 8192), (1, 4096, 6000),
                                         (16, 8192, 3000), (13, 6144, 1000), (9, 1536, 777),
+                                        (17, 8192, 3000), (32, 4608, 1000),
                                         (100, 512, 96), (300, 1024, 200), (320, 128, 8704), (450, 128, 11264)])
 def test_gateup_swiglu_vs_oracle(gpu, dt, M, K, inter):
     g = torch.Generator().manual_seed(M + K)
