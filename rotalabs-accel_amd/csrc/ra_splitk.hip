@@ -40,13 +40,19 @@
 #include "ra_internal.h"
 
 namespace ra {
+#ifdef RA_TUNING
+extern int g_sk_s, g_sk_dmax;  // tuning builds: forced split count, pipeline depth cap
+#endif
 
 namespace sk {
 constexpr int KS = 128;       // k per stage
 constexpr int NW = 4;         // waves per workgroup
 constexpr int kMaxM = 64;
 constexpr int kLds = 159 * 1024;  // rings; the rest holds the reduction flag
-constexpr int kMaxD = 6;
+// At most 3 stages in flight (<= 80 KB of LDS): measured against the deepest
+// ring that fits (6): M=17 K=28672 N=8192 48.1 vs 49.6 us, K=16384 N=4096
+// 22.4 vs 24.2, M=4 K=28672 level, M=64 K=28672 63.7 vs 62.9.
+constexpr int kMaxD = 3;
 // Counters of the split combine sit at the start of every workspace, one
 // per row block, in a fixed region (a call never writes partial sums where
 // another plan keeps a counter); plans with more row blocks do not split.
@@ -59,8 +65,8 @@ constexpr int w_slot(int tw, bool gu) { return ntw(tw, gu) * 2048; }  // per wav
 constexpr int lds_bytes(int mt, int tw, bool gu, int d) { return (d + 1) * x_slot(mt) + d * NW * w_slot(tw, gu); }
 constexpr int copies(int mt, int tw, bool gu) { return 2 * ntw(tw, gu) + mt; }  // per wave per stage
 // Deepest pipeline that fits LDS and the 6-bit vmcnt.
-constexpr int depth(int mt, int tw, bool gu) {
-  int d = kMaxD;
+constexpr int depth(int mt, int tw, bool gu, int dmax = kMaxD) {
+  int d = dmax;
   while (d > 2 && (lds_bytes(mt, tw, gu, d) > kLds || (d - 1) * copies(mt, tw, gu) > 63)) --d;
   return d;
 }
@@ -102,7 +108,7 @@ __device__ __forceinline__ void wait_stages(int younger) {
   wait_vmcnt<0>();
 }
 
-template <int DT, int MT, int TW, bool GU>
+template <int DT, int MT, int TW, bool GU, int DMAX = sk::kMaxD>
 __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__ xb, int64_t ldx,
                                                         const char *__restrict__ wb, int64_t ldw,
                                                         const float *__restrict__ scale,
@@ -115,7 +121,7 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
   constexpr int NTW = ntw(TW, GU);
   constexpr int WL = 2 * NTW;  // weight copies per stage per wave
   constexpr int CP = WL + MT;  // copies per stage per wave
-  constexpr int D = depth(MT, TW, GU);
+  constexpr int D = depth(MT, TW, GU, DMAX);
   constexpr int XS = x_slot(MT), WS = w_slot(TW, GU);
   constexpr int XRING = 0, WRING = (D + 1) * XS;
   constexpr int R = NW * TW * 16;  // output columns per unit
@@ -342,12 +348,17 @@ SplitkPlan splitk_plan(int64_t M, int64_t N, int64_t K, bool gu, bool allow_spli
   const int cus = device_cus();
   const int64_t stages = K / sk::KS;
   double best_t = 0;
+  int force_s = 0;
+#ifdef RA_TUNING
+  force_s = g_sk_s;
+#endif
   for (int tw = 1; tw <= 3; ++tw) {
     const int ntw = gu ? 2 * tw : tw;
     const int64_t R = (int64_t)sk::NW * tw * 16;
     const int64_t nb = (N + R - 1) / R;
     const int smax = (allow_split && nb <= sk::kMaxCounters) ? (int)std::min<int64_t>(stages, 16) : 1;
     for (int S = 1; S <= smax; ++S) {
+      if (force_s > 0 && S != force_s) continue;
       const int64_t kst = (stages + S - 1) / S;  // stages per split
       const int64_t se = (stages + kst - 1) / kst;
       if (se != S) continue;                     // a split would be empty
@@ -381,6 +392,15 @@ void splitk_go(const SplitkPlan &p, const void *x, int64_t ldx, const int8_t *w,
   const unsigned grid = (unsigned)(p.spread ? (int64_t)p.nb * p.S : ((p.nb + 7) / 8) * 8 * p.S);
   int *cnt = static_cast<int *>(ws);
   float *part = ws ? reinterpret_cast<float *>(static_cast<char *>(ws) + p.cnt_bytes) : nullptr;
+#ifdef RA_TUNING
+  if (g_sk_dmax == 2 || g_sk_dmax == 3) {  // forced pipeline depth cap
+    auto k = g_sk_dmax == 2 ? splitk_kernel<DT, MT, TW, GU, 2> : splitk_kernel<DT, MT, TW, GU, 3>;
+    hipLaunchKernelGGL(k, dim3(grid), dim3(256), 0, s, static_cast<const char *>(x), ldx,
+                       reinterpret_cast<const char *>(w), ldw, scale, bias, bias_dt, static_cast<uint16_t *>(y), ldy,
+                       (int)M, (int)N, (int)K, p.kc, p.S, p.nb, p.spread ? 1 : 0, part, cnt);
+    return;
+  }
+#endif
   hipLaunchKernelGGL((splitk_kernel<DT, MT, TW, GU>), dim3(grid), dim3(256), 0, s,
                      static_cast<const char *>(x), ldx, reinterpret_cast<const char *>(w), ldw, scale, bias,
                      bias_dt, static_cast<uint16_t *>(y), ldy, (int)M, (int)N, (int)K, p.kc, p.S, p.nb, p.spread ? 1 : 0,
