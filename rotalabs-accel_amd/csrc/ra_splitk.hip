@@ -148,6 +148,14 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
   const int kb = s * kc;
   const int ke = min(K, kb + kc);
   const int nst = (ke - kb) / KS;  // >= 1 (host)
+  // Row block rb walks its stages starting at stage rb % nst (wrapping), so
+  // the units in flight read different k windows. In lockstep they would all
+  // read the same window, addresses equal in their low log2(ldw) bits, which
+  // at ldw = 16384 gathers the weight stream on a few memory channels
+  // (measured M=8 K=16384 N=16384: 44.0 us against 68.2, M=16 K=32768 N=8192
+  // 43.3 against 61.3, M=8 K=8192 N=16384 26.8 against 36.7). Fixed per row
+  // block: the sums stay deterministic.
+  const int rot = rb % nst;
 
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -184,7 +192,8 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
   const uint32_t xdst = lds0 + XRING + (uint32_t)(wid * MT) * 1024;
 
   auto issue = [&](int st) __attribute__((always_inline)) {
-    const int k = kb + st * KS;
+    const int sr = st + rot < nst ? st + rot : st + rot - nst;
+    const int k = kb + sr * KS;
     const char *sw = wb + k;
     const char *sx = xb + (int64_t)k * 2;
     const uint32_t wd = wdst + (uint32_t)((st % D) * NW * WS);
