@@ -352,7 +352,9 @@ __global__ __launch_bounds__(512) void batch_xlds_kernel(const uint16_t *__restr
 //    activation rows into LDS with direct-to-LDS copies (1 KB row segments,
 //    16-byte chunks XOR-swizzled by the row) between two barriers, then
 //    streams the chunk's weights. Three workgroups share a CU (42 KB of LDS
-//    each), so the others stream while one waits for its next chunk.
+//    each), so the others stream while one waits for its next chunk. Each
+//    workgroup starts at its own chunk and wraps round, so the workgroups in
+//    flight read different k windows.
 //  * Weights in 128-k stages, per tile 2 loads of 8 rows x 128 contiguous
 //    bytes, D stages in flight (D divides the stages of a chunk), each
 //    tile's stage transposed through the wave's 2 KB LDS slot into the
@@ -383,10 +385,25 @@ __global__ __launch_bounds__(64 * gux::kWaves) void gateup_xlds_kernel(
   const int nseg = kc / 512;     // 1 KB copy segments per row and chunk
   const int spc = kc / 128;      // stages per chunk (a multiple of D)
   const int nst = K / 128;       // stages in all
+  // Workgroup b walks the chunks starting at chunk ((b >> 3) ^ (b & 7)) mod
+  // nch, wrapping (b & 7 is the XCD the hardware deals it to, b >> 3 its
+  // place there): the workgroups in flight then stream different k windows,
+  // on one XCD and across XCDs. In lockstep they all read one window, at
+  // addresses equal in their low log2(ldw) bits, which gathers the weight
+  // stream on fewer memory channels. Gate/up H=8192 I=28672 (same run):
+  // M=8 81.4 -> 73.7 us, M=16 82.5 -> 75.2, M=17 85.4 -> 78.5, M=32 94.0 ->
+  // 84.3; H=4096 I=11008 level to 5 % faster. Starting at b mod nch (XCD
+  // only) or (b >> 3) mod nch (place only) was 10-20 % slower than no
+  // rotation at M=5-8 (nch = 4).
+  const int nch = nst / spc;
+  const int rc = (((int)blockIdx.x >> 3) ^ ((int)blockIdx.x & 7)) % nch;
+  const int rs = rc * spc;  // first stage
+  auto wrap = [&](int q) __attribute__((always_inline)) { return q >= nst ? q - nst : q; };
 
-  // Weight loads: stage s of tile t (0 gate, 1 up), half hh covers rows
-  // n0 + 8hh + (lane >> 3) (+ I for up), bytes 128s + 16 (lane & 7) .. +15.
-  // Rows past I are clamped (loaded, never stored).
+  // Weight loads: the workgroup's stage s (K stage s' = (s + rs) mod nst) of
+  // tile t (0 gate, 1 up), half hh covers rows n0 + 8hh + (lane >> 3) (+ I
+  // for up), bytes 128s' + 16 (lane & 7) .. +15. Rows past I are clamped
+  // (loaded, never stored).
   const int8_t *wp[2][2];
   uint32_t wdst[2];
 #pragma unroll
@@ -401,9 +418,10 @@ __global__ __launch_bounds__(64 * gux::kWaves) void gateup_xlds_kernel(
   uint8_t *const slot = lds + gux::kXBytes + wid * gux::kSlot;
   const int xr_off = p * 128, xsw = (p >> 1) & 7;
 
-  // Copies of activation chunk c: segment sg of row m -> LDS m * row_bytes +
-  // 1024 sg, dealt to the waves in turn.
+  // Copies of the workgroup's chunk c (chunk (c + rc) mod nch of K): segment
+  // sg of row m -> LDS m * row_bytes + 1024 sg, dealt to the waves in turn.
   auto copy_chunk = [&](int c) __attribute__((always_inline)) {
+    c = c + rc < nch ? c + rc : c + rc - nch;
     for (int i = wid; i < M * nseg; i += nw) {
       const int m = i / nseg, sg = i - m * nseg;
       dma16<0, true>(x + (int64_t)m * ldx + (int64_t)c * kc + 512 * sg + 8 * (lane ^ (m & 15)),
@@ -418,7 +436,7 @@ __global__ __launch_bounds__(64 * gux::kWaves) void gateup_xlds_kernel(
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) wr[d][t][hh] = load_stream16(wp[t][hh] + 128 * d);
+      for (int hh = 0; hh < 2; ++hh) wr[d][t][hh] = load_stream16(wp[t][hh] + 128 * wrap(d + rs));
   // The copies are older than the 4*D weight loads.
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(4 * D) : "memory");
 
@@ -484,7 +502,7 @@ __global__ __launch_bounds__(64 * gux::kWaves) void gateup_xlds_kernel(
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) wr[d][t][hh] = load_stream16(wp[t][hh] + 128 * (s0 + d + D));
+        for (int hh = 0; hh < 2; ++hh) wr[d][t][hh] = load_stream16(wp[t][hh] + 128 * wrap(s0 + d + D + rs));
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -712,11 +730,18 @@ hipError_t batch_launch(const GemmArgs &a, hipStream_t s) {
 
 // gateup_xlds_kernel: M <= 32, K % 512 == 0; workgroups of 4 waves (42 KB
 // of LDS, so three share a CU and one streams while another copies its next
-// chunk); the K chunk is the largest multiple of 512 that divides K and
-// whose M activation rows fit in 34 KB. Measured (gate/up M=16 H=8192
-// I=28672, same run): 81.0 us against 89.9 with 7 waves and 4096-k chunks
-// (one workgroup per CU), 83.0 with 2048-k chunks (two per CU); 2 or 3
-// waves per workgroup 87-94.
+// chunk); the K chunk is the largest multiple of 512 that divides K, is at
+// most 2048 and whose M activation rows fit in 34 KB, except that a
+// 1024-k chunk becomes 512 when there are more workgroups than CUs.
+// Measured (gate/up M=16 H=8192 I=28672, same run, before the chunk
+// rotation): 81.0 us against 89.9 with 7 waves and 4096-k chunks (one
+// workgroup per CU), 83.0 with 2048-k chunks (two per CU); 2 or 3 waves per
+// workgroup 87-94. With the rotation (same run, three weight copies cycled;
+// chunk k 4096 / 2048 / 1024 / 512): H=8192 I=28672 (448 workgroups) M=3-4
+// 79 / 72.7 / - / 74, M=6-8 - / 73.4-74.8 / 80 / 73.9, M=12-16 - / - /
+// 81-81.5 / 75-76, M=17 - / - / 84.9 / 79.9; H=4096 I=11008 (172
+// workgroups) M=4 21.4 / 18.1 / - / 22.3, M=16 - / - / 21.0 / 23.7;
+// H=8192 I=8192 M=16 - / - / 35.9 / 40.0.
 struct GuxCfg {
   int nw = 0, kc = 0;  // waves per workgroup, k per chunk (0: not this kernel)
 };
@@ -724,11 +749,12 @@ struct GuxCfg {
 static GuxCfg gateup_xlds_cfg(const GateUpArgs &a) {
   GuxCfg c;
   if (a.M < 1 || a.M > gux::kMaxM || a.K < 512 || a.K % 512 != 0) return c;
-  int64_t kc = std::min<int64_t>(a.K, gux::kXBytes / (2 * a.M)) / 512 * 512;
+  int64_t kc = std::min<int64_t>(std::min<int64_t>(a.K, 2048), gux::kXBytes / (2 * a.M)) / 512 * 512;
   while (kc >= 512 && a.K % kc != 0) kc -= 512;
   if (kc < 512) return c;
   const int64_t blocks = (a.I + 15) / 16;
   c.nw = (int)std::min<int64_t>(gux::kWaves, blocks);
+  if (kc == 1024 && (blocks + c.nw - 1) / c.nw > device_cus()) kc = 512;
   c.kc = (int)kc;
   return c;
 }
