@@ -248,6 +248,13 @@ __global__ __launch_bounds__(512) void batch_xlds_kernel(const uint16_t *__restr
   const int n0 = blockIdx.x * (16 * RT) + 16 * tile;
   const int k0 = kp * (batchx::kSeg * RT);
   const int row_bytes = nw * (batchx::kSeg * 2);  // LDS bytes of one activation row (2K)
+  // The wave's stage s is stage (s + rot) mod ST of its K part, rot set per
+  // workgroup from its XCD (b & 7) and place there (b >> 3), so the
+  // workgroups in flight stream different k windows instead of one (same
+  // run: M=4 K=4096 N=11008 9.9 -> 9.6 us, M=8 10.2 -> 9.95, M=16 10.85 ->
+  // 10.7; N=4096 and K=2048 level).
+  const int rot = (((int)blockIdx.x >> 3) ^ ((int)blockIdx.x & 7)) % ST;
+  auto kst = [&](int q) __attribute__((always_inline)) { return q >= ST ? q - ST : q; };
 
   // Activation rows: segment wid of row j -> LDS j * row_bytes + 1024 wid.
   {
@@ -258,9 +265,9 @@ __global__ __launch_bounds__(512) void batch_xlds_kernel(const uint16_t *__restr
                      base + (uint32_t)(j * row_bytes));
   }
 
-  // Weight loads, oldest first: stage s, half h covers rows
-  // n0 + 8h + (lane >> 3), bytes k0 + 128s + 16 (lane & 7) .. +15. Rows past
-  // N are clamped (loaded, never stored).
+  // Weight loads, oldest first: stage s (K stage s' = (s + rot) mod ST),
+  // half h covers rows n0 + 8h + (lane >> 3), bytes k0 + 128s' + 16 (lane &
+  // 7) .. +15. Rows past N are clamped (loaded, never stored).
   const int8_t *wp[2];
   uint32_t wdst[2];
 #pragma unroll
@@ -278,7 +285,7 @@ __global__ __launch_bounds__(512) void batch_xlds_kernel(const uint16_t *__restr
 #pragma unroll
   for (int s = 0; s < D; ++s)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) wr[s][h] = load_stream16(wp[h] + 128 * s);
+    for (int h = 0; h < 2; ++h) wr[s][h] = load_stream16(wp[h] + 128 * kst(s + rot));
 
   // The copies are older than the 2*D weight loads: once at most 2*D loads
   // are outstanding, this wave's copies are in LDS; the barrier makes every
@@ -303,7 +310,7 @@ __global__ __launch_bounds__(512) void batch_xlds_kernel(const uint16_t *__restr
     uint4 xf[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      xf[j] = *reinterpret_cast<const uint4 *>(xrow + (((c0 + 16 * s + j) ^ sw) << 4));
+      xf[j] = *reinterpret_cast<const uint4 *>(xrow + (((c0 + 16 * kst(s + rot) + j) ^ sw) << 4));
     const uint4 X = *reinterpret_cast<const uint4 *>(slot + xr_off + (((2 * g) ^ xsw) << 4));
     const uint4 Y = *reinterpret_cast<const uint4 *>(slot + xr_off + (((2 * g + 1) ^ xsw) << 4));
     acc0 = A::mfma16(A::dq8(X.x, X.y), xf[0], acc0);
@@ -312,7 +319,7 @@ __global__ __launch_bounds__(512) void batch_xlds_kernel(const uint16_t *__restr
     acc1 = A::mfma16(A::dq8(Y.z, Y.w), xf[3], acc1);
     if (s + D < ST) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) wr[s + D][h] = load_stream16(wp[h] + 128 * (s + D));
+      for (int h = 0; h < 2; ++h) wr[s + D][h] = load_stream16(wp[h] + 128 * kst(s + D + rot));
     }
     __builtin_amdgcn_sched_barrier(0);
   }
