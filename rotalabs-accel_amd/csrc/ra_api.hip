@@ -56,11 +56,13 @@ constexpr int64_t kSplitkMinK = 16384;
 
 int select_variant(const GemmArgs &a, bool have_ws) {
   if (a.K == 0) return RA_VARIANT_GENERIC;
-  // M = 2 with 2048 <= K <= 4096: the activation-resident small-batch kernel
-  // is ahead of the row GEMV (K=4096 N=11008 9.8 vs 10.7 us, K=2048 N=11008
-  // 6.6 vs 9.0, N=4096 level); M = 1 stays with the row GEMV (8.5 vs 9.8).
-  if (a.M == 2 && batch_xlds_selected(a)) return RA_VARIANT_BATCH;
-  if (gemv_rows_supported(a)) return RA_VARIANT_ROWS;
+  // M = 2 runs the small-batch kernels where they apply: the row GEMV
+  // streams each weight row once per activation row pair no faster than
+  // the MFMA kernels (same run: K=4096 N=11008 9.6 vs 11.3 us, K=28672
+  // N=8192 40.3 split K / 38.9 small batch vs 50.0, K=16384 N=16384 44.4 /
+  // 47.4 vs 56.2, K=8192 N=57344 81.1 small batch vs 95.0). M = 1 stays with
+  // the row GEMV (8.5 vs 9.8 at K=4096 N=11008, 37.3 vs 39.0 at K=28672).
+  if (gemv_rows_supported(a) && (a.M == 1 || !batch_supported(a))) return RA_VARIANT_ROWS;
   if (have_ws && a.M <= kSkinnyMaxM && a.K >= kSplitkMinK && splitk_supported(a)) return RA_VARIANT_SPLITK;
   // M = 3..64: the small-batch kernel (line-wide weight loads, activations
   // read once per 48 rows) where K % 128 == 0, else the split-K MFMA kernel;
@@ -129,7 +131,7 @@ const char *ra_strerror(int code) {
 
 size_t ra_w8a16_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int x_dtype) {
   if (x_dtype != RA_F16 && x_dtype != RA_BF16) return 0;
-  if (M <= 2 || M > kSkinnyMaxM) return 0;  // the row GEMVs and the tiled GEMM need none
+  if (M < 2 || M > kSkinnyMaxM) return 0;  // the row GEMV (M = 1) and the tiled GEMM need none
   // (below kSplitkMinK only a forced RA_VARIANT_SPLITK launch uses it)
   const SplitkPlan p = splitk_plan(M, N, K, false, true);
   return p.ok ? p.ws_bytes : 0;
@@ -201,7 +203,7 @@ int ra_w8a16_gemm_select(int64_t M, int64_t N, int64_t K, int x_dtype) {
 
 size_t ra_w8a16_gateup_workspace_size(int64_t M, int64_t I, int64_t K, int x_dtype) {
   if (x_dtype != RA_F16 && x_dtype != RA_BF16) return 0;
-  if (M <= 2 || M > kSkinnyMaxM) return 0;
+  if (M < 2 || M > kSkinnyMaxM) return 0;
   const SplitkPlan p = splitk_plan(M, I, K, true, true);
   return p.ok ? p.ws_bytes : 0;
 }
@@ -223,7 +225,8 @@ int ra_w8a16_gateup_swiglu_ws(const void *x, int64_t ldx, int x_dtype, const int
   const GateUpArgs a{x, ldx, x_dtype, w, ldw, scale, h, ldh, M, I, K};
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool have_ws = workspace != nullptr && workspace_bytes > 0;
-  if (K > 0 && gateup_gemv_rows_supported(a)) return to_status(gateup_gemv_rows_launch(a, s));
+  if (K > 0 && gateup_gemv_rows_supported(a) && (M == 1 || !gateup_batch_supported(a)))
+    return to_status(gateup_gemv_rows_launch(a, s));
   if (K >= kSplitkMinK && have_ws && M <= kSkinnyMaxM && gateup_splitk_supported(a)) {
     const SplitkPlan p = splitk_plan(M, I, K, true, true);
     if (p.ok) {

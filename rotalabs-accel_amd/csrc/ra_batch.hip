@@ -710,10 +710,6 @@ static void batch_xlds_dispatch(const GemmArgs &a, int rt, hipStream_t s) {
   batch_xlds_go<DT, 4>(a, s);
 }
 
-bool batch_xlds_selected(const GemmArgs &a) {
-  return batch_supported(a) && batch_xlds_rt(a, device_cus()) > 0;
-}
-
 hipError_t batch_launch(const GemmArgs &a, hipStream_t s) {
   int xrt = batch_xlds_rt(a, device_cus());
 #ifdef RA_TUNING

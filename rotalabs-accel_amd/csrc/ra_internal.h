@@ -72,8 +72,6 @@ hipError_t gateup_gemv_rows_launch(const GateUpArgs &a, hipStream_t s);
 // transposed through LDS, split-K across the workgroup's waves.
 bool batch_supported(const GemmArgs &a);
 hipError_t batch_launch(const GemmArgs &a, hipStream_t s);
-// Whether batch_launch runs its activation-resident kernel for this shape.
-bool batch_xlds_selected(const GemmArgs &a);
 bool gateup_batch_supported(const GateUpArgs &a);
 hipError_t gateup_batch_launch(const GateUpArgs &a, hipStream_t s);
 

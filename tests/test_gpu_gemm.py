@@ -283,10 +283,11 @@ def test_tiled_tile_geometries(gpu, M, K, N, dt):
 
 
 # Split-K small-batch shapes: many splits (long K, few rows), N tails, one
-# stage per split, every activation-tile count (M <= 16, 32, 64) and the
-# cfg-3 / cfg-5 decode shapes.
+# stage per split, every activation-tile count (M <= 16, 32, 64), two rows,
+# and the small-batch (K=4096 N=11008) and MLP down-projection shapes.
 SPLITK_SHAPES = [(3, 4096, 11008), (16, 4096, 11008), (64, 4096, 11008), (8, 8192, 256), (17, 8192, 300),
-                 (33, 1024, 1000), (64, 128, 64), (5, 28672, 8192), (20, 2048, 77), (40, 512, 3000)]
+                 (33, 1024, 1000), (64, 128, 64), (5, 28672, 8192), (20, 2048, 77), (40, 512, 3000),
+                 (2, 16384, 700)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
@@ -338,16 +339,21 @@ def test_splitk_selected_for_long_k():
     assert lib.ra_w8a16_gemm_select(64, 4096, 4096, _backend.F16) == BATCH
 
 
-def test_two_rows_take_the_activation_resident_kernel():
-    """M = 2 runs the small-batch kernel where its activation-resident form
-    applies (2048 <= K <= 4096), else the row GEMV; M = 1 the row GEMV."""
+def test_two_rows_take_the_small_batch_kernels():
+    """M = 2 runs the small-batch kernels wherever they apply (K % 128 == 0;
+    split K from K = 16384 with a workspace), the row GEMV only where they
+    do not; M = 1 the row GEMV."""
     lib = _backend.load()
     assert lib.ra_w8a16_gemm_select(2, 11008, 4096, _backend.F16) == BATCH
     assert lib.ra_w8a16_gemm_select(2, 4096, 2048, _backend.BF16) == BATCH
-    assert lib.ra_w8a16_gemm_select(2, 4096, 11008, _backend.F16) == ROWS
-    assert lib.ra_w8a16_gemm_select(2, 4096, 1024, _backend.F16) == ROWS
+    assert lib.ra_w8a16_gemm_select(2, 4096, 11008, _backend.F16) == BATCH
+    assert lib.ra_w8a16_gemm_select(2, 4096, 1024, _backend.F16) == BATCH
+    assert lib.ra_w8a16_gemm_select(2, 8192, 28672, _backend.BF16) == SPLITK
+    assert lib.ra_w8a16_gemm_select(2, 4096, 1040, _backend.F16) == ROWS
     assert lib.ra_w8a16_gemm_select(1, 11008, 4096, _backend.F16) == ROWS
-    assert lib.ra_w8a16_gemm_workspace_size(2, 11008, 4096, _backend.F16) == 0
+    assert lib.ra_w8a16_gemm_select(1, 8192, 28672, _backend.F16) == ROWS
+    assert lib.ra_w8a16_gemm_workspace_size(2, 8192, 28672, _backend.BF16) > 0
+    assert lib.ra_w8a16_gemm_workspace_size(1, 8192, 28672, _backend.BF16) == 0
 
 
 @pytest.mark.parametrize("M", [1, 16, 2048])
