@@ -28,6 +28,7 @@ int g_batch_xlds = 0;
 int g_batch_xd = 0;
 int g_sk_s = 0;
 int g_sk_dmax = 0;
+int g_tiled_split = 0;
 int g_w8a8_mode = 0;
 int g_rows_lds = 0;
 }
@@ -92,7 +93,10 @@ int check_gemm(const GemmArgs &a) {
 namespace ra {
 // Workspace bytes the automatic selection uses for this GEMM (0: none).
 size_t auto_workspace_bytes(const GemmArgs &a) {
-  if (a.M == 0 || a.N == 0 || select_variant(a, true) != RA_VARIANT_SPLITK) return 0;
+  if (a.M == 0 || a.N == 0) return 0;
+  const int v = select_variant(a, true);
+  if (v == RA_VARIANT_TILED) return tiled_split_plan(a).ws_bytes;
+  if (v != RA_VARIANT_SPLITK) return 0;
   const SplitkPlan p = splitk_plan(a.M, a.N, a.K, false, true);
   return p.ok ? p.ws_bytes : 0;
 }
@@ -110,6 +114,7 @@ void ra_tune_batch_nw(int nw) { ra::g_batch_nw = nw; }
 void ra_tune_batch_xlds(int v) { ra::g_batch_xlds = v; }
 void ra_tune_batch_xd(int v) { ra::g_batch_xd = v; }
 void ra_tune_sk(int s, int dmax) { ra::g_sk_s = s; ra::g_sk_dmax = dmax; }
+void ra_tune_tiled_split(int v) { ra::g_tiled_split = v; }
 void ra_tune_w8a8(int mode) { ra::g_w8a8_mode = mode; }
 void ra_tune_rows_lds(int v) { ra::g_rows_lds = v; }
 #endif
@@ -131,10 +136,16 @@ const char *ra_strerror(int code) {
 
 size_t ra_w8a16_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int x_dtype) {
   if (x_dtype != RA_F16 && x_dtype != RA_BF16) return 0;
-  if (M < 2 || M > kSkinnyMaxM) return 0;  // the row GEMV (M = 1) and the tiled GEMM need none
-  // (below kSplitkMinK only a forced RA_VARIANT_SPLITK launch uses it)
+  if (M < 2 || M > kSkinnyMaxM) return 0;  // the row GEMV (M = 1) and the large-M tiled GEMM need none
+  // The split-K kernel's plan (below kSplitkMinK only a forced
+  // RA_VARIANT_SPLITK launch uses it) or, at M = 33..64, the small tile's
+  // split plan, whichever needs more (contiguous, aligned operands).
   const SplitkPlan p = splitk_plan(M, N, K, false, true);
-  return p.ok ? p.ws_bytes : 0;
+  const GemmArgs a{reinterpret_cast<const void *>(256), K, x_dtype, reinterpret_cast<const int8_t *>(256),
+                   K, nullptr, nullptr, RA_F32, nullptr, N, M, N, K};
+  const size_t tiled = tiled_split_plan(a).ws_bytes;
+  const size_t sk = p.ok ? p.ws_bytes : 0;
+  return sk > tiled ? sk : tiled;
 }
 
 int ra_w8a16_gemm_ex(const void *x, int64_t ldx, int x_dtype, const int8_t *w, int64_t ldw,
@@ -171,7 +182,7 @@ int ra_w8a16_gemm_ex(const void *x, int64_t ldx, int x_dtype, const int8_t *w, i
       return to_status(batch_launch(a, s));
     case RA_VARIANT_TILED:
       if (!tiled_supported(a) || K == 0) return RA_ERR_VARIANT;
-      return to_status(tiled_launch(a, s));
+      return to_status(tiled_launch_ws(a, have_ws ? workspace : nullptr, workspace_bytes, s));
     case RA_VARIANT_GENERIC:
       return to_status(generic_launch(a, s));
     default:

@@ -294,4 +294,19 @@ __device__ __forceinline__ float epilogue_value(float acc, const float *scale, c
   return v;
 }
 
+// 16-byte buffer stores and loads at device scope (cache policy sc1): written
+// through to, and read from, the level all XCDs share, so partial sums pass
+// between workgroups on any XCD without a cache-wide fence. Buffer
+// instructions, so the compiler tracks their waits; out-of-range offsets
+// read zeros and drop stores.
+constexpr int kCpolSc1 = 16;
+constexpr int kRsrcWord3 = 0x00020000;  // raw (untyped) buffer, gfx9 family
+typedef unsigned int u32x4_dev __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store_dev16(__amdgpu_buffer_rsrc_t r, uint32_t off, const f32x4 &v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_dev, v), r, (int)off, 0, kCpolSc1);
+}
+__device__ __forceinline__ f32x4 load_dev16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kCpolSc1));
+}
+
 }  // namespace ra

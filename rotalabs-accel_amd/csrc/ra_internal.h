@@ -40,6 +40,18 @@ bool tiled_supported(const GemmArgs &a);
 // (M = 33..64, at least 8192 weight rows, K % 64 == 0).
 bool tiled_small_selected(const GemmArgs &a);
 hipError_t tiled_launch(const GemmArgs &a, hipStream_t s);
+// M = 33..64 (where tiled_small_selected): the small tile with K split over
+// workgroups, when the plan beats the 64 x 64 tile over all of K (nsplit >
+// 1 needs ws_bytes of workspace, laid out as the split-K kernel's: the
+// counter block first). tiled_launch_ws runs it when it applies and the
+// workspace suffices, else tiled_launch.
+struct TiledSplitPlan {
+  bool ok = false;
+  int bnb = 0, nsplit = 1, ksplit = 0;
+  size_t ws_bytes = 0;
+};
+TiledSplitPlan tiled_split_plan(const GemmArgs &a);
+hipError_t tiled_launch_ws(const GemmArgs &a, void *ws, size_t ws_bytes, hipStream_t s);
 
 // Generic kernel: any shape, alignment and activation dtype.
 hipError_t generic_launch(const GemmArgs &a, hipStream_t s);

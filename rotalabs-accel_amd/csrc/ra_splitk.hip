@@ -81,21 +81,6 @@ __device__ __forceinline__ void dma16s_nt(const void *sbase, uint32_t voff, uint
                : "memory", "m0");
 }
 
-// 16-byte buffer stores and loads at device scope (cache policy sc1): written
-// through to, and read from, the level all XCDs share, so partial sums pass
-// between workgroups on any XCD without a cache-wide fence. Buffer
-// instructions, so the compiler tracks their waits; out-of-range offsets
-// read zeros and drop stores.
-constexpr int kCpolSc1 = 16;
-constexpr int kRsrcWord3 = 0x00020000;  // raw (untyped) buffer, gfx9 family
-typedef unsigned int u32x4_sk __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void store_dev16(__amdgpu_buffer_rsrc_t r, uint32_t off, const f32x4 &v) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_sk, v), r, (int)off, 0, kCpolSc1);
-}
-__device__ __forceinline__ f32x4 load_dev16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kCpolSc1));
-}
-
 // Wait until at most `younger` stages of CP copies are in flight for this wave.
 template <int CP, int D>
 __device__ __forceinline__ void wait_stages(int younger) {
@@ -264,27 +249,37 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
       s_last = __hip_atomic_fetch_add(&cnt[rb], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
     __syncthreads();
     if (!s_last) return;
-    // Sum the splits in order 0..S-1 (this unit's from registers); each
-    // split's fragments are loaded together, then added.
+    // Sum the splits in order 0..S-1 (this unit's from registers). The
+    // fragments of CHK splits at a time are loaded together (one round trip
+    // per CHK splits, at most 16 fragments in flight), then added in order.
+    constexpr int CHK = NTW * MT >= 16 ? 1 : (16 / (NTW * MT) >= 4 ? 4 : 16 / (NTW * MT));
     f32x4 sum[NTW][MT];
-    for (int s2 = 0; s2 < S; ++s2) {
-      f32x4 v[NTW][MT];
-      if (s2 == s) {
+    for (int s0 = 0; s0 < S; s0 += CHK) {
+      f32x4 v[CHK][NTW][MT];
 #pragma unroll
-        for (int t = 0; t < NTW; ++t)
+      for (int j = 0; j < CHK; ++j) {
+        const int s2 = s0 + j;
+        if (s2 < S && s2 != s) {
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) v[t][mt] = acc[t][mt];
-      } else {
+          for (int t = 0; t < NTW; ++t)
 #pragma unroll
-        for (int t = 0; t < NTW; ++t)
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            v[t][mt] = load_dev16(rs, lo + (uint32_t)(s2 * NW * FR + (t * MT + mt) * 256) * 4u);
+            for (int mt = 0; mt < MT; ++mt)
+              v[j][t][mt] = load_dev16(rs, lo + (uint32_t)(s2 * NW * FR + (t * MT + mt) * 256) * 4u);
+        }
       }
 #pragma unroll
-      for (int t = 0; t < NTW; ++t)
+      for (int j = 0; j < CHK; ++j) {
+        const int s2 = s0 + j;
+        if (s2 < S) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) sum[t][mt] = s2 == 0 ? v[t][mt] : sum[t][mt] + v[t][mt];
+          for (int t = 0; t < NTW; ++t)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const f32x4 cur = s2 == s ? acc[t][mt] : v[j][t][mt];
+              sum[t][mt] = s2 == 0 ? cur : sum[t][mt] + cur;
+            }
+        }
+      }
     }
 #pragma unroll
     for (int t = 0; t < NTW; ++t)

@@ -268,7 +268,7 @@ struct DmaTile {
   static constexpr int B_COPIES = B_BYTES / 4096;
   static constexpr int COPIES = A_COPIES + B_COPIES;
   // pipeline depth: up to 4 stages, up to SMAX for small tiles
-  static constexpr int SMAX = STAGE <= 16 * 1024 ? SMAX_SMALL : 4;
+  static constexpr int SMAX = STAGE <= 24 * 1024 ? SMAX_SMALL : 4;
   static constexpr int S = (160 * 1024) / STAGE < SMAX ? (160 * 1024) / STAGE : SMAX;
   static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "copies must split evenly over 4 waves");
   static_assert(S >= 2 && S <= 8, "2 to 8 stages");
@@ -288,13 +288,25 @@ __device__ __forceinline__ void wait_tiles(int younger) {
   }
 }
 
-template <int DT, bool GU, int BMB, int BNB, int WR, int SM = 4>
+// SPLIT (M <= 64, one row of tiles): K is split over nsplit workgroups per
+// tile, ksplit K tiles each (the last may have fewer); workgroup b runs split
+// b % nsplit of tile b / nsplit. With nsplit > 1 each writes its fp32 sums
+// to the workspace with device-scope stores, waits for them and counts
+// itself in on the tile's counter (device-scope atomic); the workgroup that
+// completes the count adds the nsplit partial sums in split order
+// (deterministic), runs the epilogue and resets the counter. No workgroup
+// waits for another. Partial sums: [tile][split][wave][BMB*BNB*4 chunks of
+// 4][64 lanes][4 floats]; counters: one int per tile at cnt.
+constexpr int kMaxTileSplits = 4;  // K splits per tile of the SPLIT form
+
+template <int DT, bool GU, int BMB, int BNB, int WR, int SM = 4, bool SPLIT = false>
 __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__restrict__ x, int64_t ldx,
                                                            const int8_t *__restrict__ w, int64_t ldw,
                                                            const float *__restrict__ scale,
                                                            const void *__restrict__ bias, int bias_dt,
                                                            uint16_t *__restrict__ y, int64_t ldy, int M, int N,
-                                                           int K, int tiles_m, int tiles_n) {
+                                                           int K, int tiles_m, int tiles_n, int nsplit, int ksplit,
+                                                           float *__restrict__ part, int *__restrict__ cnt) {
   using G = DmaTile<BMB, BNB, WR, SM>;
   using Ac = Act<DT>;
   constexpr int BM = G::BM, BN = G::BN, BK = G::BK, WM = G::WM, WN = G::WN, S = G::S;
@@ -308,7 +320,9 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
 
   // ---- tile coordinates (XCD-aware, grouped along M as in tiled_kernel) ----
   const int T = tiles_m * tiles_n;
-  const int b = blockIdx.x;
+  const int b = SPLIT ? (int)blockIdx.x / nsplit : (int)blockIdx.x;
+  const int sp = SPLIT ? (int)blockIdx.x - b * nsplit : 0;  // K split of this workgroup
+  const int kt0 = sp * ksplit;                               // its first K tile
   const int xcd = b & 7, idx = b >> 3;
   const int per = T >> 3, rem = T & 7;
   const int t = xcd * per + (xcd < rem ? xcd : rem) + idx;
@@ -376,8 +390,8 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
 // part and of each group. The K tile's byte offset goes into the SGPR base.
 #define RA_ISSUE_PART(kt_, st_, LO_, HI_)                                                   \
   {                                                                                         \
-    const char *sa_ = xb + (int64_t)(kt_) * (2 * BK);                                       \
-    const char *sb_ = wb + (int64_t)(kt_) * BK;                                             \
+    const char *sa_ = xb + (int64_t)(kt0 + (kt_)) * (2 * BK);                               \
+    const char *sb_ = wb + (int64_t)(kt0 + (kt_)) * BK;                                     \
     const uint32_t so_ = (uint32_t)(st_) * STAGE;                                           \
     static_for_int<LO_, HI_>([&](auto ic_) {                                                    \
       constexpr int i = decltype(ic_)::value;                                               \
@@ -502,7 +516,7 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
   });                                                                                               \
   __builtin_amdgcn_sched_barrier(0);
 
-  const int KT = K / BK;
+  const int KT = SPLIT ? min(K / BK - kt0, ksplit) : K / BK;  // K tiles of this workgroup (>= 1)
 #pragma unroll
   for (int s = 0; s < S; ++s)
     if (s < KT) RA_ISSUE(s, s);
@@ -560,6 +574,58 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
 #undef RA_READ_A
 #undef RA_ISSUE
 #undef RA_ISSUE_PART
+
+  if constexpr (SPLIT) {
+    if (nsplit > 1) {
+      // Partial sums through the level all XCDs share (sc1 stores / loads).
+      __shared__ int s_last;
+      constexpr int CH = BMB * BNB * 4;  // 16-byte chunks per lane
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          part + (size_t)t * nsplit * 4 * CH * 256, 0, nsplit * 4 * CH * 256 * (int)sizeof(float), kRsrcWord3);
+      auto off = [&](int split, int c) { return (uint32_t)((((split * 4 + wid) * CH + c) * 64 + lane) * 16); };
+#pragma unroll
+      for (int bi = 0; bi < BMB; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < BNB; ++bj)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x16 &a = acc[bi][bj];
+            store_dev16(rs, off(sp, (bi * BNB + bj) * 4 + q), f32x4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]});
+          }
+      wait_vmcnt<0>();  // this wave's partial sums are stored
+      __syncthreads();  // and every wave's
+      if (tid == 0) s_last = __hip_atomic_fetch_add(&cnt[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+      __syncthreads();
+      if (!s_last) return;
+      // Sum the splits in order 0..nsplit-1 (this workgroup's from
+      // registers): every other split's chunks are loaded at once (one
+      // round trip; loading split by split cost a round trip each), then
+      // added in order.
+      f32x4 o[kMaxTileSplits][BMB * BNB * 4];
+#pragma unroll
+      for (int s2 = 0; s2 < kMaxTileSplits; ++s2)
+#pragma unroll
+        for (int c = 0; c < BMB * BNB * 4; ++c)
+          if (s2 < nsplit && s2 != sp) o[s2][c] = load_dev16(rs, off(s2, c));
+#pragma unroll
+      for (int bi = 0; bi < BMB; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < BNB; ++bj)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int c = (bi * BNB + bj) * 4 + q;
+            const f32x16 &a = acc[bi][bj];
+            const f32x4 own{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+            f32x4 v = sp == 0 ? own : o[0][c];
+#pragma unroll
+            for (int s2 = 1; s2 < kMaxTileSplits; ++s2)
+              if (s2 < nsplit) v += s2 == sp ? own : o[s2][c];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[bi][bj][4 * q + e] = v[e];
+          }
+      if (tid == 0) __hip_atomic_store(&cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 
   // ---- epilogue: scale (+ bias) or the gate/up SwiGLU on the fp32 sums ----
   // Lane (l32, g) holds, for block (bi, bj), column l32 of rows
@@ -667,6 +733,79 @@ bool tiled_small_selected(const GemmArgs &a) {
          a.K % tiled::BK == 0 && tiled_supported(a) && dma_span_ok(false, a.ldx, a.ldw, a.N, a.K, 256);
 }
 
+static int device_cus();
+
+// Split-K plans for the small tile (M = 33..64): 64-row tiles of 64*bnb
+// weight rows (2 x 2 waves of bnb 32x32 blocks), K split over nsplit
+// workgroups per tile. Time model fitted to the same-run times of every
+// (bnb, nsplit) at 15 shapes (M = 33..64, K = 2048..14336, N = 8192..28672):
+// a workgroup takes a_bnb + 16 us per MB it copies (64*bnb weight rows and 64
+// activation rows of 128 B per K tile), a = 6 / 10 / 12 us for bnb = 1 / 2
+// / 3, in rounds of one workgroup per CU, plus 2 us for the combine when
+// nsplit > 1. It picks the fastest measured configuration at 13 of the 15
+// and is within 0.6 us at the other two; e.g. M=64 K=11008 N=8192 27.6 us
+// (bnb 2, 4 splits) against 51.3 for the 64 x 64 tile over all of K, K=8192
+// N=11008 28.9 against 35.0, K=4096 N=28672 32.7 against 38.4; K=4096
+// N=11008 keeps the 64 x 64 tile (19.6 us; the best split 19.4).
+constexpr double kTileUs[4] = {0.0, 6.0, 10.0, 12.0};  // a_bnb
+constexpr double kTileUsPerMB = 16.0;
+constexpr double kTileCombineUs = 2.0;
+#ifdef RA_TUNING
+extern int g_tiled_split;  // tuning builds: -1 never split, 10*bnb + nsplit forced
+#endif
+
+TiledSplitPlan tiled_split_plan(const GemmArgs &a) {
+  TiledSplitPlan best{};
+  if (!tiled_small_selected(a)) return best;
+  if ((uint64_t)((a.N - 1) * a.ldw + a.K) > DMA_SPAN) return best;  // one launch covers all of W
+  const int cus = device_cus();
+  const int64_t KT = a.K / tiled::BK;
+  auto cost = [&](int bnb, int nsplit, int64_t ksplit) {
+    const int64_t tiles = (a.N + 64 * bnb - 1) / (64 * bnb);
+    const int64_t rounds = (tiles * nsplit + cus - 1) / cus;
+    const double mb = (double)(64 * bnb + 128) * 64 * ksplit * 1e-6;
+    return (double)rounds * (kTileUs[bnb] + kTileUsPerMB * mb) + (nsplit > 1 ? kTileCombineUs : 0.0);
+  };
+  double best_t = cost(1, 1, KT);  // the 64 x 64 tile over all of K
+  int force = 0;
+#ifdef RA_TUNING
+  force = g_tiled_split;
+  if (force < 0) return best;
+#endif
+  for (int bnb = 1; bnb <= 3; ++bnb) {
+    for (int nsplit = 1; nsplit <= kMaxTileSplits; ++nsplit) {
+      if (bnb == 1 && nsplit == 1) continue;
+      if (force > 0 && force != 10 * bnb + nsplit) continue;
+      const int64_t tiles = (a.N + 64 * bnb - 1) / (64 * bnb);
+      const int64_t ksplit = (KT + nsplit - 1) / nsplit;
+      if ((nsplit - 1) * ksplit >= KT) continue;  // a split would be empty
+      if (nsplit > 1 && tiles > (int64_t)(kSplitkCounterBytes / sizeof(int))) continue;
+      const double t = cost(bnb, nsplit, ksplit);
+      if (force > 0 || t < best_t) {
+        best.ok = true;
+        best.bnb = bnb;
+        best.nsplit = nsplit;
+        best.ksplit = (int)ksplit;
+        best.ws_bytes = nsplit > 1 ? kSplitkCounterBytes + (size_t)tiles * nsplit * 4 * (bnb * 4) * 256 * sizeof(float) : 0;
+        best_t = t;
+      }
+    }
+  }
+  return best;
+}
+
+template <int DT, int BNB>
+static void launch_dma_split(const GemmArgs &a, const TiledSplitPlan &p, void *ws, hipStream_t s) {
+  using G = DmaTile<1, BNB, 2, 6>;
+  const int tiles_n = (int)((a.N + G::BN - 1) / G::BN);
+  int *cnt = static_cast<int *>(ws);
+  float *part = p.nsplit > 1 ? reinterpret_cast<float *>(static_cast<char *>(ws) + kSplitkCounterBytes) : nullptr;
+  hipLaunchKernelGGL((tiled_dma_kernel<DT, false, 1, BNB, 2, 6, true>), dim3((unsigned)(tiles_n * p.nsplit)),
+                     dim3(256), 0, s, static_cast<const uint16_t *>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias,
+                     a.bias_dt, static_cast<uint16_t *>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K, 1, tiles_n,
+                     p.nsplit, p.ksplit, part, cnt);
+}
+
 template <int DT, bool GU, int BMB, int BNB, int WR, int SM = 4>
 static void launch_dma(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
                        const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
@@ -688,7 +827,7 @@ static void launch_dma(const void *x, int64_t ldx, const int8_t *w, int64_t ldw,
       const int tiles_n = (int)((Ni + OUTN - 1) / OUTN);
       hipLaunchKernelGGL((tiled_dma_kernel<DT, GU, BMB, BNB, WR, SM>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s,
                          xi, ldx, w + ns * ldw, ldw, si, bi, bias_dt, yi, ldy, (int)Mi, (int)Ni, (int)K, tiles_m,
-                         tiles_n);
+                         tiles_n, 1, 0, nullptr, nullptr);
     }
   }
 }
@@ -800,6 +939,22 @@ static hipError_t launch(const void *x, int64_t ldx, int x_dt, const int8_t *w, 
 hipError_t tiled_launch(const GemmArgs &a, hipStream_t s) {
   return launch<false>(a.x, a.ldx, a.x_dt, a.w, a.ldw, a.scale, a.bias, a.bias_dt, a.y, a.ldy, a.M, a.N, a.K,
                        s);
+}
+
+hipError_t tiled_launch_ws(const GemmArgs &a, void *ws, size_t ws_bytes, hipStream_t s) {
+  const TiledSplitPlan p = tiled_split_plan(a);
+  if (!p.ok || (p.nsplit > 1 && (!ws || ws_bytes < p.ws_bytes))) return tiled_launch(a, s);
+#define RA_SPLIT_GO(BNB_)                                                          \
+  if (p.bnb == BNB_) {                                                             \
+    if (a.x_dt == RA_F16) launch_dma_split<RA_F16, BNB_>(a, p, ws, s);             \
+    else launch_dma_split<RA_BF16, BNB_>(a, p, ws, s);                             \
+    return hipGetLastError();                                                      \
+  }
+  RA_SPLIT_GO(1)
+  RA_SPLIT_GO(2)
+  RA_SPLIT_GO(3)
+#undef RA_SPLIT_GO
+  return tiled_launch(a, s);
 }
 
 bool gateup_tiled_supported(const GateUpArgs &a) {

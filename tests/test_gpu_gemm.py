@@ -180,6 +180,32 @@ def test_exact_known_answer_small_tile(gpu, M, K, N, dt):
         assert torch.equal(y, want), f"variant {v}: {(y.double() - exact).abs().max()}"
 
 
+# M = 33..64 shapes whose plan splits K over workgroups or widens the tile
+# (64 x 64*bnb tiles, nsplit splits; bnb/nsplit from the plan at 256 CUs):
+# 2/4, 2/3, 3/4, 3/2, 3/1, 2/2, 2/1, 1/2 -- K tiles not a multiple of the
+# split count, N tails, the partial sums of up to four splits combined.
+SPLIT_TILE_SHAPES = [(33, 9216, 8192), (64, 8192, 9000), (50, 6144, 12000), (64, 4096, 16500), (48, 1024, 40000),
+                     (64, 6144, 16384), (40, 2048, 24000), (64, 6144, 8192)]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K,N", SPLIT_TILE_SHAPES)
+def test_exact_known_answer_split_tile(gpu, M, K, N, dt):
+    """The small tile with K split over workgroups, their fp32 partial sums
+    combined in the workspace: exact known answers, forced and automatic
+    (two calls in a row: a tile counter left non-zero would leave the second
+    call's tiles unwritten)."""
+    lib = _backend.load()
+    assert lib.ra_w8a16_gemm_select(M, N, K, _backend.dtype_code(dt)) == TILED
+    x, q, s, b, exact = _exact_case(M, K, N, dt, seed=7 * M + K + N, dev=gpu, bias=(N % 2 == 0))
+    print(f"  split tiles M={M} K={K} N={N} {dt} workspace "
+          f"{lib.ra_w8a16_gemm_workspace_size(M, N, K, _backend.dtype_code(dt))} B", flush=True)
+    want = exact.to(dt)
+    for v in (TILED, _backend.VARIANT_AUTO):
+        y = _run(x, q, s, b, v).cpu()
+        assert torch.equal(y, want), f"variant {v}: {(y.double() - exact).abs().max()}"
+
+
 def test_exact_fp32_activations(gpu):
     x, q, s, b, exact = _exact_case(9, 200, 70, torch.float32, seed=5, dev=gpu, bias=True)
     y = _run(x, q, s, b).cpu()

@@ -1,8 +1,9 @@
 """ra_w8a16_gemm_noalloc, the entry point that allocates nothing (its split-K
 workspace is the library's fixed device array), through the C ABI: equal
 bit for bit to ra_w8a16_gemm_ws with a caller workspace, on two calls in a
-row, the second on a smaller problem; a problem needing more than the
-array is refused (tests/test_abi.py)."""
+row, the second on a smaller problem, then a call whose tiled kernel splits
+K over workgroups (the same array holds its partial sums); a problem needing
+more than the array is refused (tests/test_abi.py)."""
 import pytest
 import torch
 
@@ -22,12 +23,14 @@ def _args(c, y):
 def test_noalloc_matches_workspace_entry_point(gpu):
     lib = _backend.load()
     stream = torch.cuda.current_stream(gpu).cuda_stream
-    # (M, K, N, seed): the MLP's down projection at M=17, then a smaller split-K problem
-    for (M, K, N, seed) in [(17, 28672, 8192, 1), (5, 16384, 1000, 2)]:
+    # (M, K, N, seed): the MLP's down projection at M=17, then a smaller split-K
+    # problem, then the 64-row tiles with K split over four workgroups
+    for (M, K, N, seed) in [(17, 28672, 8192, 1), (5, 16384, 1000, 2), (64, 8192, 11008, 3)]:
         print(f"  noalloc M={M} K={K} N={N}", flush=True)
         c = gemm_case(M, K, N, seed, device=gpu, dtype=torch.bfloat16, outlier_rows=True)
         xdt = _backend.dtype_code(c.x.dtype)
-        assert lib.ra_w8a16_gemm_select(M, N, K, xdt) == _backend.VARIANT_SPLITK
+        assert lib.ra_w8a16_gemm_select(M, N, K, xdt) == (_backend.VARIANT_TILED if M == 64 else
+                                                          _backend.VARIANT_SPLITK)
         need = lib.ra_w8a16_gemm_workspace_size(M, N, K, xdt)
         assert 0 < need <= 16 << 20
         ws = torch.zeros(need, dtype=torch.uint8, device=gpu)
