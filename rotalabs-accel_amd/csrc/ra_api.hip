@@ -92,6 +92,10 @@ int check_gemm(const GemmArgs &a) {
 
 namespace ra {
 // Workspace bytes the automatic selection uses for this GEMM (0: none).
+bool auto_workspace_optional(const GemmArgs &a) {
+  return a.M > 0 && a.N > 0 && select_variant(a, true) == RA_VARIANT_TILED;
+}
+
 size_t auto_workspace_bytes(const GemmArgs &a) {
   if (a.M == 0 || a.N == 0) return 0;
   const int v = select_variant(a, true);

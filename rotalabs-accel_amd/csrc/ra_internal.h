@@ -106,8 +106,11 @@ bool gateup_splitk_supported(const GateUpArgs &a);
 hipError_t gateup_splitk_launch(const GateUpArgs &a, const SplitkPlan &p, void *ws, hipStream_t s);
 
 // Workspace bytes the automatic kernel selection of ra_w8a16_gemm_ws uses
-// for this problem (0: the selected kernel needs none).
+// for this problem (0: the selected kernel needs none), and whether that
+// kernel also runs without it (the tiled kernel's split plan is optional:
+// with less workspace it runs its tile over all of K).
 size_t auto_workspace_bytes(const GemmArgs &a);
+bool auto_workspace_optional(const GemmArgs &a);
 
 // Decode GEMV (M <= 4, x staged in LDS, one HBM round trip per wave).
 bool gemv_supported(const GemmArgs &a);

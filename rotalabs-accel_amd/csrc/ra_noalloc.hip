@@ -1,7 +1,8 @@
 // ra_w8a16_gemm_noalloc: ra_w8a16_gemm_ws for callers that cannot allocate
 // (code under HIP graph capture, serving loops that forbid allocation). The
-// split-K small-batch kernel's workspace is a fixed device array of this
-// library instead of a caller buffer; nothing is allocated or freed.
+// workspace of the small-batch kernels that split K (the split-K kernel,
+// the tiled kernel's split plan) is a fixed device array of this library
+// instead of a caller buffer; nothing is allocated or freed.
 //
 //  * `scratch` is a file-scope device array, one per GPU the library runs on
 //    (each holds its own copy at its own address until the process ends).
@@ -65,8 +66,11 @@ extern "C" int ra_w8a16_gemm_noalloc(const void *x, int64_t ldx, int x_dtype, co
   if (M < 0 || N < 0 || K < 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return RA_ERR_ARG;
   if (M == 0 || N == 0) return ra_w8a16_gemm_ws(x, ldx, x_dtype, w, ldw, scale, bias, bias_dtype, y, ldy, M, N, K,
                                                 nullptr, 0, stream);
-  const size_t need = (x_dtype == RA_F16 || x_dtype == RA_BF16) ? ra::auto_workspace_bytes(a) : 0;
-  if (need > kScratchBytes) return RA_ERR_WORKSPACE;
+  size_t need = (x_dtype == RA_F16 || x_dtype == RA_BF16) ? ra::auto_workspace_bytes(a) : 0;
+  if (need > kScratchBytes) {
+    if (!ra::auto_workspace_optional(a)) return RA_ERR_WORKSPACE;
+    need = 0;  // the tiled kernel runs its tile over all of K instead
+  }
   void *ws = nullptr;
   size_t ws_bytes = 0;
   if (need > 0) {
