@@ -110,8 +110,19 @@ def dtype_code(dtype: torch.dtype) -> int:
                         "(float16, bfloat16 and float32 are supported)") from None
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
 def stream_handle(device: torch.device) -> int:
-    """hipStream_t of torch's current stream on ``device`` (as an integer)."""
+    """hipStream_t of torch's current stream on ``device`` (as an integer).
+    Read without building a Stream object where torch offers that (the
+    object costs ~1.7 us of host time per call)."""
+    if _raw_stream is not None:
+        return _raw_stream(_device_index(device))
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -132,8 +143,7 @@ def workspace(device: torch.device, nbytes: int):
     steps when a larger problem needs more."""
     if nbytes <= 0:
         return None, 0
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    key = (idx, torch.cuda.current_stream(device).cuda_stream)
+    key = (_device_index(device), stream_handle(device))
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         size = -(-nbytes // _WS_ROUND) * _WS_ROUND

@@ -43,6 +43,10 @@ def _rows(t: torch.Tensor, align: int) -> tuple[torch.Tensor, int]:
     """Return (t2, ld): a 2-D view with unit column stride and row stride ld
     (in elements) whose rows start on ``align``-byte boundaries when the row
     length allows it; copies only when ``t`` is not already laid out so."""
+    if t.is_contiguous() and t.data_ptr() % align == 0:  # the common case, checked cheaply
+        cols = t.shape[1]
+        if (cols * t.element_size()) % align == 0 or t.shape[0] <= 1:
+            return t, cols
     rows, cols = t.shape
     ld = t.stride(0) if rows > 1 else cols
     esz = t.element_size()
@@ -106,7 +110,7 @@ def _int8_gemm_hip(x: torch.Tensor, weight_int8: torch.Tensor, scale: torch.Tens
     K = x.shape[-1]
     N = weight_int8.shape[0]
     xdt = _backend.dtype_code(x.dtype)
-    x2, ldx = _rows(x.reshape(-1, K), align=16)
+    x2, ldx = _rows(x if x.dim() == 2 else x.reshape(-1, K), align=16)
     M = x2.shape[0]
     w, ldw = _rows(weight_int8, align=16)
     s = scale if (scale.dtype == torch.float32 and scale.is_contiguous()) else scale.float().contiguous()
@@ -121,7 +125,7 @@ def _int8_gemm_hip(x: torch.Tensor, weight_int8: torch.Tensor, scale: torch.Tens
     _backend.check(code)
     if post_bias is not None:
         y.add_(post_bias)
-    return y.view(*x.shape[:-1], N)
+    return y if x.dim() == 2 else y.view(*x.shape[:-1], N)
 
 
 def int8_gemm(
