@@ -89,6 +89,19 @@ def test_variant_selection_fallbacks():
     assert lib.ra_w8a16_gemm_select(4, 64, 0, 0) == 3      # K == 0 -> generic (bias / zeros)
 
 
+def test_workspace_of_the_tiled_split_plan():
+    """M = 33..64 shapes whose tiled plan splits K (64 x 128 tiles over 4
+    workgroups at M=64 K=11008 N=8192) ask for a workspace; the 64 x 64 tile
+    over all of K (K=4096 N=11008) and large M need none from the tiled
+    kernel (the size reported there is the split-K kernel's plan, for a forced
+    RA_VARIANT_SPLITK launch)."""
+    lib = _backend.load()
+    assert lib.ra_w8a16_gemm_select(64, 8192, 11008, 0) == 2
+    assert lib.ra_w8a16_gemm_workspace_size(64, 8192, 11008, 0) >= 16384 + 64 * 4 * 32768
+    assert lib.ra_w8a16_gemm_workspace_size(2048, 11008, 4096, 0) == 0
+    assert lib.ra_w8a16_gemm_workspace_size(1, 11008, 4096, 0) == 0
+
+
 def test_w8a8_argument_checks_without_device_work():
     lib = _backend.load()
     n = None
