@@ -619,11 +619,21 @@ static int row1_windows(int64_t K, bool gu) {
 
 template <int DT, bool GU, int CH>
 static void row1_go(const RowsParams &p, hipStream_t s) {
-  const int wpg = p.N <= 8192 ? 8 : 4;  // as rows_lds_go
+  // 4 waves per workgroup at every N (same run, against 8 up to N = 8192:
+  // K=11008 N=4096 9.08 vs 9.30 us, K=14336 N=4096 11.1 vs 11.3, K=8192
+  // N=8192 11.6 vs 11.8, K=5120 N=5120 6.10 vs 6.35; 16: 6-15 % slower).
+  int wpg = 4;
+#ifdef RA_TUNING
+  extern int g_rows_lds;  // > 0: waves per workgroup
+  if (g_rows_lds == 4 || g_rows_lds == 8 || g_rows_lds == 16) wpg = g_rows_lds;
+#endif
 #define RA_ROW1_GO(WPG_)                                                                                     \
   hipLaunchKernelGGL((gemv_row1_kernel<DT, GU, WPG_, CH>), dim3((unsigned)((p.N + WPG_ - 1) / WPG_)),       \
                      dim3(64 * WPG_), (size_t)2048 * ((p.K + 1023) / 1024), s, p.x, p.w, p.ldw, p.scale, p.bias, p.bias_dt, p.N, p.K, \
                      p.y)
+#ifdef RA_TUNING
+  if (wpg == 16) { RA_ROW1_GO(16); return; }
+#endif
   if (wpg == 8) RA_ROW1_GO(8);
   else RA_ROW1_GO(4);
 #undef RA_ROW1_GO
