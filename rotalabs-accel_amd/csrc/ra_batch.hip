@@ -678,7 +678,7 @@ static int batch_xlds_rt(const GemmArgs &a, int cus) {
   if (a.M < 1 || a.M > batchx::kMaxM || a.K % batchx::kSeg != 0) return 0;
   const int64_t nw = a.K / batchx::kSeg;
   if (nw < batchx::kMinWaves || nw > batchx::kMaxWaves) return 0;
-  for (int rt = 1; rt <= 4; ++rt)
+  for (int rt : {1, 2, 3, 4, 6, 8})  // the instantiated tile counts
     if (nw % rt == 0 && (a.N + 16 * rt - 1) / (16 * rt) <= cus) return rt;
   return 0;
 }
@@ -707,7 +707,9 @@ static void batch_xlds_dispatch(const GemmArgs &a, int rt, hipStream_t s) {
   if (rt == 1) return batch_xlds_go<DT, 1>(a, s);
   if (rt == 2) return batch_xlds_go<DT, 2>(a, s);
   if (rt == 3) return batch_xlds_go<DT, 3>(a, s);
-  batch_xlds_go<DT, 4>(a, s);
+  if (rt == 4) return batch_xlds_go<DT, 4>(a, s);
+  if (rt == 6) return batch_xlds_go<DT, 6>(a, s);
+  batch_xlds_go<DT, 8>(a, s);
 }
 
 hipError_t batch_launch(const GemmArgs &a, hipStream_t s) {

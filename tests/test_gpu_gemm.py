@@ -119,12 +119,12 @@ def test_exact_known_answer_wide_batch(gpu, M, K, N, dt):
 # Shapes the small-batch kernel with the activation rows resident in LDS
 # takes (M <= 16, K = 2048 .. 4096 in steps of 512, K / 512 waves shared
 # equally by the workgroup's 16-row weight tiles, at most one workgroup per
-# CU): 1, 2, 3 or 4 tiles per workgroup, 1 to 7 K parts per tile, 2 or 4
-# stages in flight, M from 1 to 16, N tails inside a tile and a half-filled
-# last tile.
+# CU): 1, 2, 3, 4, 6 or 8 tiles per workgroup, 1 to 7 K parts per tile (a
+# single part at 6 and 8 tiles), 2 or 4 stages in flight, M from 1 to 16, N
+# tails inside a tile and a half-filled last tile.
 XLDS_SHAPES = [(1, 2048, 16), (2, 4096, 64), (3, 3072, 77), (5, 4096, 11008), (8, 2560, 4000), (13, 2048, 300),
                (16, 4096, 11008), (16, 3584, 4096), (11, 2048, 8193), (16, 2048, 14000), (7, 3072, 12000),
-               (6, 4096, 6000), (16, 3072, 9000)]
+               (6, 4096, 6000), (16, 3072, 9000), (2, 4096, 28672), (16, 4096, 20000), (9, 3072, 24000)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
