@@ -64,11 +64,19 @@ int select_variant(const GemmArgs &a, bool have_ws) {
   // 47.4 vs 56.2, K=8192 N=57344 81.1 small batch vs 95.0). M = 1 stays with
   // the row GEMV (8.5 vs 9.8 at K=4096 N=11008, 37.3 vs 39.0 at K=28672).
   if (gemv_rows_supported(a) && (a.M == 1 || !batch_supported(a))) return RA_VARIANT_ROWS;
-  if (have_ws && a.M <= kSkinnyMaxM && a.K >= kSplitkMinK && splitk_supported(a)) return RA_VARIANT_SPLITK;
+  // M = 33..64 with at least 8192 weight rows: the 64-row tiles (K split
+  // over workgroups where that pays), also at long K (M=64 K=28672 N=8192:
+  // 58.0 us against 65.9 for the split-K kernel).
+  if (tiled_small_selected(a)) return RA_VARIANT_TILED;
+  // Split K: long K, or from 16 rows K >= 11008 over at most 4096 weight
+  // rows (M=64 K=14336 N=4096: 29.1 us against 55.0 for the small-batch
+  // kernel, M=16 K=11008 N=4096 15.0 against 16.3).
+  if (have_ws && a.M <= kSkinnyMaxM && splitk_supported(a) &&
+      (a.K >= kSplitkMinK || (a.M >= 16 && a.K >= 11008 && a.N <= 4096)))
+    return RA_VARIANT_SPLITK;
   // M = 3..64: the small-batch kernel (line-wide weight loads, activations
   // read once per 48 rows) where K % 128 == 0, else the split-K MFMA kernel;
   // both measured faster than the LDS GEMV, which stays as a fallback.
-  if (tiled_small_selected(a)) return RA_VARIANT_TILED;
   if (a.M <= kSkinnyMaxM && batch_supported(a)) return RA_VARIANT_BATCH;
   if (a.M <= kSkinnyMaxM && skinny_supported(a)) return RA_VARIANT_SKINNY;
   if (gemv_supported(a)) return RA_VARIANT_GEMV;
@@ -140,10 +148,10 @@ const char *ra_strerror(int code) {
 
 size_t ra_w8a16_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int x_dtype) {
   if (x_dtype != RA_F16 && x_dtype != RA_BF16) return 0;
-  if (M < 2 || M > kSkinnyMaxM) return 0;  // the row GEMV (M = 1) and the large-M tiled GEMM need none
-  // The split-K kernel's plan (below kSplitkMinK only a forced
-  // RA_VARIANT_SPLITK launch uses it) or, at M = 33..64, the small tile's
-  // split plan, whichever needs more (contiguous, aligned operands).
+  if (M < 2 || M > 128) return 0;  // the row GEMV (M = 1) and the large-M tiled GEMM need none
+  // The split-K kernel's plan (M <= 64; where it is not selected only a
+  // forced RA_VARIANT_SPLITK launch uses it) or, at M = 33..128, the 64-row
+  // tiles' split plan, whichever needs more (contiguous, aligned operands).
   const SplitkPlan p = splitk_plan(M, N, K, false, true);
   const GemmArgs a{reinterpret_cast<const void *>(256), K, x_dtype, reinterpret_cast<const int8_t *>(256),
                    K, nullptr, nullptr, RA_F32, nullptr, N, M, N, K};

@@ -41,10 +41,11 @@ bool tiled_supported(const GemmArgs &a);
 bool tiled_small_selected(const GemmArgs &a);
 hipError_t tiled_launch(const GemmArgs &a, hipStream_t s);
 // M = 33..64 (where tiled_small_selected): the small tile with K split over
-// workgroups, when the plan beats the 64 x 64 tile over all of K (nsplit >
-// 1 needs ws_bytes of workspace, laid out as the split-K kernel's: the
-// counter block first). tiled_launch_ws runs it when it applies and the
-// workspace suffices, else tiled_launch.
+// workgroups, when the plan beats the 64 x 64 tile over all of K; M =
+// 65..128: two rows of these tiles, the best plan (nsplit > 1 needs ws_bytes
+// of workspace, laid out as the split-K kernel's: the counter block first).
+// tiled_launch_ws runs it when it applies and the workspace suffices, else
+// tiled_launch.
 struct TiledSplitPlan {
   bool ok = false;
   int bnb = 0, nsplit = 1, ksplit = 0;

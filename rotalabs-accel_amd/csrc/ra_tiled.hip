@@ -288,7 +288,7 @@ __device__ __forceinline__ void wait_tiles(int younger) {
   }
 }
 
-// SPLIT (M <= 64, one row of tiles): K is split over nsplit workgroups per
+// SPLIT (M <= 128, one or two rows of tiles): K is split over nsplit workgroups per
 // tile, ksplit K tiles each (the last may have fewer); workgroup b runs split
 // b % nsplit of tile b / nsplit. With nsplit > 1 each writes its fp32 sums
 // to the workspace with device-scope stores, waits for them and counts
@@ -733,6 +733,17 @@ bool tiled_small_selected(const GemmArgs &a) {
          a.K % tiled::BK == 0 && tiled_supported(a) && dma_span_ok(false, a.ldx, a.ldw, a.N, a.K, 256);
 }
 
+// M = 65..128: the large tiles leave most CUs idle where N is small (M=128
+// K=11008 N=4096: 16 tiles of 256 x 256), so these run two rows of the 64-row
+// split tiles too.
+constexpr int64_t kSplitTileMaxM = 128;
+
+static bool tiled_split_eligible(const GemmArgs &a) {
+  if (tiled_small_selected(a)) return true;
+  return a.M > kSmallTileMaxM && a.M <= kSplitTileMaxM && a.K > 0 && a.K % tiled::BK == 0 &&
+         tiled_supported(a) && dma_span_ok(false, a.ldx, a.ldw, a.N, a.K, 256);
+}
+
 static int device_cus();
 
 // Split-K plans for the small tile (M = 33..64): 64-row tiles of 64*bnb
@@ -756,17 +767,21 @@ extern int g_tiled_split;  // tuning builds: -1 never split, 10*bnb + nsplit for
 
 TiledSplitPlan tiled_split_plan(const GemmArgs &a) {
   TiledSplitPlan best{};
-  if (!tiled_small_selected(a)) return best;
+  if (!tiled_split_eligible(a)) return best;
   if ((uint64_t)((a.N - 1) * a.ldw + a.K) > DMA_SPAN) return best;  // one launch covers all of W
   const int cus = device_cus();
   const int64_t KT = a.K / tiled::BK;
+  const int64_t tiles_m = (a.M + 63) / 64;
   auto cost = [&](int bnb, int nsplit, int64_t ksplit) {
-    const int64_t tiles = (a.N + 64 * bnb - 1) / (64 * bnb);
+    const int64_t tiles = tiles_m * ((a.N + 64 * bnb - 1) / (64 * bnb));
     const int64_t rounds = (tiles * nsplit + cus - 1) / cus;
     const double mb = (double)(64 * bnb + 128) * 64 * ksplit * 1e-6;
     return (double)rounds * (kTileUs[bnb] + kTileUsPerMB * mb) + (nsplit > 1 ? kTileCombineUs : 0.0);
   };
-  double best_t = cost(1, 1, KT);  // the 64 x 64 tile over all of K
+  // Up to 64 rows the split plans compete with the 64 x 64 tile over all of
+  // K (the launch without a workspace); above, the best plan is taken.
+  const bool one_row = tiles_m == 1;
+  double best_t = one_row ? cost(1, 1, KT) : 0.0;
   int force = 0;
 #ifdef RA_TUNING
   force = g_tiled_split;
@@ -774,14 +789,14 @@ TiledSplitPlan tiled_split_plan(const GemmArgs &a) {
 #endif
   for (int bnb = 1; bnb <= 3; ++bnb) {
     for (int nsplit = 1; nsplit <= kMaxTileSplits; ++nsplit) {
-      if (bnb == 1 && nsplit == 1) continue;
+      if (one_row && bnb == 1 && nsplit == 1) continue;
       if (force > 0 && force != 10 * bnb + nsplit) continue;
-      const int64_t tiles = (a.N + 64 * bnb - 1) / (64 * bnb);
+      const int64_t tiles = tiles_m * ((a.N + 64 * bnb - 1) / (64 * bnb));
       const int64_t ksplit = (KT + nsplit - 1) / nsplit;
       if ((nsplit - 1) * ksplit >= KT) continue;  // a split would be empty
       if (nsplit > 1 && tiles > (int64_t)(kSplitkCounterBytes / sizeof(int))) continue;
       const double t = cost(bnb, nsplit, ksplit);
-      if (force > 0 || t < best_t) {
+      if (force > 0 || (!best.ok && !one_row) || t < best_t) {
         best.ok = true;
         best.bnb = bnb;
         best.nsplit = nsplit;
@@ -798,11 +813,12 @@ template <int DT, int BNB>
 static void launch_dma_split(const GemmArgs &a, const TiledSplitPlan &p, void *ws, hipStream_t s) {
   using G = DmaTile<1, BNB, 2, 6>;
   const int tiles_n = (int)((a.N + G::BN - 1) / G::BN);
+  const int tiles_m = (int)((a.M + G::BM - 1) / G::BM);
   int *cnt = static_cast<int *>(ws);
   float *part = p.nsplit > 1 ? reinterpret_cast<float *>(static_cast<char *>(ws) + kSplitkCounterBytes) : nullptr;
-  hipLaunchKernelGGL((tiled_dma_kernel<DT, false, 1, BNB, 2, 6, true>), dim3((unsigned)(tiles_n * p.nsplit)),
+  hipLaunchKernelGGL((tiled_dma_kernel<DT, false, 1, BNB, 2, 6, true>), dim3((unsigned)(tiles_m * tiles_n * p.nsplit)),
                      dim3(256), 0, s, static_cast<const uint16_t *>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias,
-                     a.bias_dt, static_cast<uint16_t *>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K, 1, tiles_n,
+                     a.bias_dt, static_cast<uint16_t *>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K, tiles_m, tiles_n,
                      p.nsplit, p.ksplit, part, cnt);
 }
 

@@ -66,9 +66,10 @@ def test_argument_checks_without_device_work():
     assert lib.ra_w8a16_gemm_workspace_size(2048, 11008, 4096, 0) == 0   # tiled: none
     assert lib.ra_w8a16_gateup_swiglu_ws(n, 0, 0, n, 0, n, n, 0, 0, 8, 8, n, 0, n) == 0
     # the no-allocation entry point refuses a problem whose split-K workspace exceeds its
-    # 16 MiB array (M=64 K=16384 N=57344 needs ~73 MB) before any launch; argument errors as usual
-    assert lib.ra_w8a16_gemm_workspace_size(64, 57344, 16384, 0) > 16 << 20
-    assert lib.ra_w8a16_gemm_noalloc(p, 16384, 0, p, 16384, p, n, 0, p, 57344, 64, 57344, 16384, n) == 6
+    # 16 MiB array (M=32 K=16384 N=57344 needs ~35 MB) before any launch; argument errors as usual
+    assert lib.ra_w8a16_gemm_select(32, 57344, 16384, 0) == 7
+    assert lib.ra_w8a16_gemm_workspace_size(32, 57344, 16384, 0) > 16 << 20
+    assert lib.ra_w8a16_gemm_noalloc(p, 16384, 0, p, 16384, p, n, 0, p, 57344, 32, 57344, 16384, n) == 6
     assert lib.ra_w8a16_gemm_noalloc(n, 0, 0, n, 0, n, n, 0, n, 0, -1, 4, 4, n) == 1
     assert lib.ra_w8a16_gemm_noalloc(n, 0, 0, n, 0, n, n, 0, n, 0, 0, 4, 4, n) == 0
 
@@ -83,6 +84,10 @@ def test_variant_selection_fallbacks():
     assert lib.ra_w8a16_gemm_select(1, 8192, 28672, 1) == 5  # row GEMV: any K
     assert lib.ra_w8a16_gemm_select(3, 8192, 8192, 1) == 6   # M = 3..64, K % 128 == 0: small-batch kernel
     assert lib.ra_w8a16_gemm_select(17, 8192, 28672, 1) == 7  # ... with K >= 16384: split K over workgroups
+    assert lib.ra_w8a16_gemm_select(16, 4096, 11008, 1) == 7  # ... from 16 rows, K >= 11008 over N <= 4096
+    assert lib.ra_w8a16_gemm_select(15, 4096, 11008, 1) == 6
+    assert lib.ra_w8a16_gemm_select(16, 4097, 11008, 1) == 6
+    assert lib.ra_w8a16_gemm_select(64, 8192, 28672, 1) == 2  # M = 33..64, N >= 8192: 64-row tiles
     assert lib.ra_w8a16_gemm_select(4, 8192, 1040, 1) == 1   # K % 128 != 0: split-K MFMA kernel
     assert lib.ra_w8a16_gemm_select(1, 64, 50, 0) == 3     # K % 16 != 0 -> generic
     assert lib.ra_w8a16_gemm_select(1, 64, 64, 2) == 3     # fp32 activations -> generic
@@ -100,6 +105,12 @@ def test_workspace_of_the_tiled_split_plan():
     assert lib.ra_w8a16_gemm_workspace_size(64, 8192, 11008, 0) >= 16384 + 64 * 4 * 32768
     assert lib.ra_w8a16_gemm_workspace_size(2048, 11008, 4096, 0) == 0
     assert lib.ra_w8a16_gemm_workspace_size(1, 11008, 4096, 0) == 0
+    # M = 65..128: two rows of 64-row tiles; at K=11008 N=4096 (32 tiles of
+    # 64 x 128) the plan splits K, so it asks for a workspace; from M = 129 none
+    assert lib.ra_w8a16_gemm_select(128, 4096, 11008, 0) == 2
+    assert lib.ra_w8a16_gemm_workspace_size(128, 4096, 11008, 0) > 16384
+    assert lib.ra_w8a16_gemm_workspace_size(65, 4096, 11008, 0) > 16384
+    assert lib.ra_w8a16_gemm_workspace_size(129, 4096, 11008, 0) == 0
 
 
 def test_w8a8_argument_checks_without_device_work():

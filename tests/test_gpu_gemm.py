@@ -185,7 +185,9 @@ def test_exact_known_answer_small_tile(gpu, M, K, N, dt):
 # 2/4, 2/3, 3/4, 3/2, 3/1, 2/2, 2/1, 1/2 -- K tiles not a multiple of the
 # split count, N tails, the partial sums of up to four splits combined.
 SPLIT_TILE_SHAPES = [(33, 9216, 8192), (64, 8192, 9000), (50, 6144, 12000), (64, 4096, 16500), (48, 1024, 40000),
-                     (64, 6144, 16384), (40, 2048, 24000), (64, 6144, 8192)]
+                     (64, 6144, 16384), (40, 2048, 24000), (64, 6144, 8192),
+                     # M = 65..128: two rows of tiles (ragged M and N; the last without a K split)
+                     (65, 2048, 4096), (100, 11008, 4096), (128, 4096, 8200), (80, 6144, 9000), (97, 1024, 3000)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
