@@ -48,7 +48,7 @@ hipError_t tiled_launch(const GemmArgs &a, hipStream_t s);
 // tiled_launch.
 struct TiledSplitPlan {
   bool ok = false;
-  int bnb = 0, nsplit = 1, ksplit = 0;
+  int bmb = 1, bnb = 0, nsplit = 1, ksplit = 0;  // tiles of 64*bmb x 64*bnb
   size_t ws_bytes = 0;
 };
 TiledSplitPlan tiled_split_plan(const GemmArgs &a);

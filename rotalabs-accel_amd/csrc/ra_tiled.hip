@@ -288,6 +288,15 @@ __device__ __forceinline__ void wait_tiles(int younger) {
   }
 }
 
+// The K-tile byte offset of the copies' SGPR base: the 128-row split tiles
+// need it marked uniform (else it can land in VGPRs, which the copy's SGPR
+// operand cannot take).
+template <bool RFL>
+__device__ __forceinline__ int uniform_if(int v) {
+  if constexpr (RFL) return __builtin_amdgcn_readfirstlane(v);
+  else return v;
+}
+
 // SPLIT (M <= 128, one or two rows of tiles): K is split over nsplit workgroups per
 // tile, ksplit K tiles each (the last may have fewer); workgroup b runs split
 // b % nsplit of tile b / nsplit. With nsplit > 1 each writes its fp32 sums
@@ -298,6 +307,7 @@ __device__ __forceinline__ void wait_tiles(int younger) {
 // waits for another. Partial sums: [tile][split][wave][BMB*BNB*4 chunks of
 // 4][64 lanes][4 floats]; counters: one int per tile at cnt.
 constexpr int kMaxTileSplits = 4;  // K splits per tile of the SPLIT form
+constexpr int kMaxTileBmb = 2;     // 32x32 row blocks per wave of the SPLIT form (tiles of 64 or 128 rows)
 
 template <int DT, bool GU, int BMB, int BNB, int WR, int SM = 4, bool SPLIT = false>
 __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__restrict__ x, int64_t ldx,
@@ -390,8 +400,9 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
 // part and of each group. The K tile's byte offset goes into the SGPR base.
 #define RA_ISSUE_PART(kt_, st_, LO_, HI_)                                                   \
   {                                                                                         \
-    const char *sa_ = xb + (int64_t)(kt0 + (kt_)) * (2 * BK);                               \
-    const char *sb_ = wb + (int64_t)(kt0 + (kt_)) * BK;                                     \
+    const int ko_ = uniform_if<SPLIT && (BMB > 1)>((kt0 + (kt_)) * BK);                     \
+    const char *sa_ = xb + (int64_t)ko_ * 2;                                                \
+    const char *sb_ = wb + (int64_t)ko_;                                                    \
     const uint32_t so_ = (uint32_t)(st_) * STAGE;                                           \
     static_for_int<LO_, HI_>([&](auto ic_) {                                                    \
       constexpr int i = decltype(ic_)::value;                                               \
@@ -600,29 +611,32 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
       // Sum the splits in order 0..nsplit-1 (this workgroup's from
       // registers): every other split's chunks are loaded at once (one
       // round trip; loading split by split cost a round trip each), then
-      // added in order.
-      f32x4 o[kMaxTileSplits][BMB * BNB * 4];
+      // added in order; above 12 chunks per lane (128-row tiles) in groups
+      // of 8, one round trip each, to bound the registers they take.
+      constexpr int NC = BMB * BNB * 4;
+      constexpr int CG = NC <= 12 ? NC : 8;
 #pragma unroll
-      for (int s2 = 0; s2 < kMaxTileSplits; ++s2)
+      for (int g0 = 0; g0 < NC; g0 += CG) {
+        f32x4 o[kMaxTileSplits][CG];
 #pragma unroll
-        for (int c = 0; c < BMB * BNB * 4; ++c)
-          if (s2 < nsplit && s2 != sp) o[s2][c] = load_dev16(rs, off(s2, c));
+        for (int s2 = 0; s2 < kMaxTileSplits; ++s2)
 #pragma unroll
-      for (int bi = 0; bi < BMB; ++bi)
+          for (int c = 0; c < CG; ++c)
+            if (g0 + c < NC && s2 < nsplit && s2 != sp) o[s2][c] = load_dev16(rs, off(s2, g0 + c));
 #pragma unroll
-        for (int bj = 0; bj < BNB; ++bj)
+        for (int c = 0; c < CG; ++c) {
+          if (g0 + c >= NC) break;
+          const int bi = (g0 + c) / (BNB * 4), bj = (g0 + c) / 4 % BNB, q = (g0 + c) % 4;
+          const f32x16 &a = acc[bi][bj];
+          const f32x4 own{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+          f32x4 v = sp == 0 ? own : o[0][c];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int c = (bi * BNB + bj) * 4 + q;
-            const f32x16 &a = acc[bi][bj];
-            const f32x4 own{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
-            f32x4 v = sp == 0 ? own : o[0][c];
+          for (int s2 = 1; s2 < kMaxTileSplits; ++s2)
+            if (s2 < nsplit) v += s2 == sp ? own : o[s2][c];
 #pragma unroll
-            for (int s2 = 1; s2 < kMaxTileSplits; ++s2)
-              if (s2 < nsplit) v += s2 == sp ? own : o[s2][c];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[bi][bj][4 * q + e] = v[e];
-          }
+          for (int e = 0; e < 4; ++e) acc[bi][bj][4 * q + e] = v[e];
+        }
+      }
       if (tid == 0) __hip_atomic_store(&cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -761,6 +775,18 @@ static int device_cus();
 constexpr double kTileUs[4] = {0.0, 6.0, 10.0, 12.0};  // a_bnb
 constexpr double kTileUsPerMB = 16.0;
 constexpr double kTileCombineUs = 2.0;
+// M = 65..128 (two rows of 64-row tiles, or one row of 128-row tiles, bmb =
+// 2): the same form refitted (least squares on relative error) to the
+// same-run times of all 24 (bmb, bnb, nsplit) at M = 65 / 96 / 128 over 7
+// (K, N) from K=2048 N=8192 to K=28672 N=8192: a = 1.9 / 7.9 / 10.3 us for
+// bmb = 1 and 5.8 / 12.3 / 18.6 for bmb = 2 (bnb = 1 / 2 / 3), 18.8 us per
+// MB, 4.5 us for the combine. Its pick is the fastest at 12 of the 21 and
+// 4 % off on average (worst 18 %, K=8192 N=8192 at M=128); e.g. M=128
+// K=28672 N=8192 83.1 us (128 x 128 tiles in 4 splits) against 97.5 for the
+// 64-row tiles' plan, K=4096 N=28672 44.4 against 57.8.
+constexpr double kTile2Us[3][4] = {{0, 0, 0, 0}, {0.0, 1.9, 7.9, 10.3}, {0.0, 5.8, 12.3, 18.6}};
+constexpr double kTile2UsPerMB = 18.8;
+constexpr double kTile2CombineUs = 4.5;
 #ifdef RA_TUNING
 extern int g_tiled_split;  // tuning builds: -1 never split, 10*bnb + nsplit forced
 #endif
@@ -772,51 +798,58 @@ TiledSplitPlan tiled_split_plan(const GemmArgs &a) {
   const int cus = device_cus();
   const int64_t KT = a.K / tiled::BK;
   const int64_t tiles_m = (a.M + 63) / 64;
-  auto cost = [&](int bnb, int nsplit, int64_t ksplit) {
-    const int64_t tiles = tiles_m * ((a.N + 64 * bnb - 1) / (64 * bnb));
+  auto cost = [&](int bmb, int bnb, int nsplit, int64_t ksplit) {
+    const int64_t tiles = (tiles_m + bmb - 1) / bmb * ((a.N + 64 * bnb - 1) / (64 * bnb));
     const int64_t rounds = (tiles * nsplit + cus - 1) / cus;
-    const double mb = (double)(64 * bnb + 128) * 64 * ksplit * 1e-6;
+    const double mb = (double)(64 * bnb + 128 * bmb) * 64 * ksplit * 1e-6;
+    if (tiles_m > 1)
+      return (double)rounds * (kTile2Us[bmb][bnb] + kTile2UsPerMB * mb) + (nsplit > 1 ? kTile2CombineUs : 0.0);
     return (double)rounds * (kTileUs[bnb] + kTileUsPerMB * mb) + (nsplit > 1 ? kTileCombineUs : 0.0);
   };
   // Up to 64 rows the split plans compete with the 64 x 64 tile over all of
   // K (the launch without a workspace); above, the best plan is taken.
   const bool one_row = tiles_m == 1;
-  double best_t = one_row ? cost(1, 1, KT) : 0.0;
+  double best_t = one_row ? cost(1, 1, 1, KT) : 0.0;
   int force = 0;
 #ifdef RA_TUNING
   force = g_tiled_split;
   if (force < 0) return best;
 #endif
-  for (int bnb = 1; bnb <= 3; ++bnb) {
-    for (int nsplit = 1; nsplit <= kMaxTileSplits; ++nsplit) {
-      if (one_row && bnb == 1 && nsplit == 1) continue;
-      if (force > 0 && force != 10 * bnb + nsplit) continue;
-      const int64_t tiles = tiles_m * ((a.N + 64 * bnb - 1) / (64 * bnb));
-      const int64_t ksplit = (KT + nsplit - 1) / nsplit;
-      if ((nsplit - 1) * ksplit >= KT) continue;  // a split would be empty
-      if (nsplit > 1 && tiles > (int64_t)(kSplitkCounterBytes / sizeof(int))) continue;
-      const double t = cost(bnb, nsplit, ksplit);
-      if (force > 0 || (!best.ok && !one_row) || t < best_t) {
-        best.ok = true;
-        best.bnb = bnb;
-        best.nsplit = nsplit;
-        best.ksplit = (int)ksplit;
-        best.ws_bytes = nsplit > 1 ? kSplitkCounterBytes + (size_t)tiles * nsplit * 4 * (bnb * 4) * 256 * sizeof(float) : 0;
-        best_t = t;
+  for (int bmb = 1; bmb <= kMaxTileBmb; ++bmb) {
+    if (bmb > 1 && one_row) break;
+    for (int bnb = 1; bnb <= 3; ++bnb) {
+      for (int nsplit = 1; nsplit <= kMaxTileSplits; ++nsplit) {
+        if (one_row && bnb == 1 && nsplit == 1) continue;
+        if (bmb == 2 && bnb == 1 && force == 0) continue;  // 128 x 64: never the model's pick where measured
+        if (force > 0 && force != 100 * (bmb - 1) + 10 * bnb + nsplit) continue;
+        const int64_t tiles = (tiles_m + bmb - 1) / bmb * ((a.N + 64 * bnb - 1) / (64 * bnb));
+        const int64_t ksplit = (KT + nsplit - 1) / nsplit;
+        if ((nsplit - 1) * ksplit >= KT) continue;  // a split would be empty
+        if (nsplit > 1 && tiles > (int64_t)(kSplitkCounterBytes / sizeof(int))) continue;
+        const double t = cost(bmb, bnb, nsplit, ksplit);
+        if (force > 0 || (!best.ok && !one_row) || t < best_t) {
+          best.ok = true;
+          best.bmb = bmb;
+          best.bnb = bnb;
+          best.nsplit = nsplit;
+          best.ksplit = (int)ksplit;
+          best.ws_bytes = nsplit > 1 ? kSplitkCounterBytes + (size_t)tiles * nsplit * 4 * (bmb * bnb * 4) * 256 * sizeof(float) : 0;
+          best_t = t;
+        }
       }
     }
   }
   return best;
 }
 
-template <int DT, int BNB>
+template <int DT, int BMB, int BNB>
 static void launch_dma_split(const GemmArgs &a, const TiledSplitPlan &p, void *ws, hipStream_t s) {
-  using G = DmaTile<1, BNB, 2, 6>;
+  using G = DmaTile<BMB, BNB, 2, 6>;
   const int tiles_n = (int)((a.N + G::BN - 1) / G::BN);
   const int tiles_m = (int)((a.M + G::BM - 1) / G::BM);
   int *cnt = static_cast<int *>(ws);
   float *part = p.nsplit > 1 ? reinterpret_cast<float *>(static_cast<char *>(ws) + kSplitkCounterBytes) : nullptr;
-  hipLaunchKernelGGL((tiled_dma_kernel<DT, false, 1, BNB, 2, 6, true>), dim3((unsigned)(tiles_m * tiles_n * p.nsplit)),
+  hipLaunchKernelGGL((tiled_dma_kernel<DT, false, BMB, BNB, 2, 6, true>), dim3((unsigned)(tiles_m * tiles_n * p.nsplit)),
                      dim3(256), 0, s, static_cast<const uint16_t *>(a.x), a.ldx, a.w, a.ldw, a.scale, a.bias,
                      a.bias_dt, static_cast<uint16_t *>(a.y), a.ldy, (int)a.M, (int)a.N, (int)a.K, tiles_m, tiles_n,
                      p.nsplit, p.ksplit, part, cnt);
@@ -960,15 +993,20 @@ hipError_t tiled_launch(const GemmArgs &a, hipStream_t s) {
 hipError_t tiled_launch_ws(const GemmArgs &a, void *ws, size_t ws_bytes, hipStream_t s) {
   const TiledSplitPlan p = tiled_split_plan(a);
   if (!p.ok || (p.nsplit > 1 && (!ws || ws_bytes < p.ws_bytes))) return tiled_launch(a, s);
-#define RA_SPLIT_GO(BNB_)                                                          \
-  if (p.bnb == BNB_) {                                                             \
-    if (a.x_dt == RA_F16) launch_dma_split<RA_F16, BNB_>(a, p, ws, s);             \
-    else launch_dma_split<RA_BF16, BNB_>(a, p, ws, s);                             \
+#define RA_SPLIT_GO(BMB_, BNB_)                                                    \
+  if (p.bmb == BMB_ && p.bnb == BNB_) {                                            \
+    if (a.x_dt == RA_F16) launch_dma_split<RA_F16, BMB_, BNB_>(a, p, ws, s);       \
+    else launch_dma_split<RA_BF16, BMB_, BNB_>(a, p, ws, s);                       \
     return hipGetLastError();                                                      \
   }
-  RA_SPLIT_GO(1)
-  RA_SPLIT_GO(2)
-  RA_SPLIT_GO(3)
+  RA_SPLIT_GO(1, 1)
+  RA_SPLIT_GO(1, 2)
+  RA_SPLIT_GO(1, 3)
+#ifdef RA_TUNING
+  RA_SPLIT_GO(2, 1)
+#endif
+  RA_SPLIT_GO(2, 2)
+  RA_SPLIT_GO(2, 3)
 #undef RA_SPLIT_GO
   return tiled_launch(a, s);
 }

@@ -186,8 +186,10 @@ def test_exact_known_answer_small_tile(gpu, M, K, N, dt):
 # split count, N tails, the partial sums of up to four splits combined.
 SPLIT_TILE_SHAPES = [(33, 9216, 8192), (64, 8192, 9000), (50, 6144, 12000), (64, 4096, 16500), (48, 1024, 40000),
                      (64, 6144, 16384), (40, 2048, 24000), (64, 6144, 8192),
-                     # M = 65..128: two rows of tiles (ragged M and N; the last without a K split)
-                     (65, 2048, 4096), (100, 11008, 4096), (128, 4096, 8200), (80, 6144, 9000), (97, 1024, 3000)]
+                     # M = 65..128: two rows of 64-row tiles or one row of 128-row tiles (ragged M
+                     # and N; 128 x 128 and 128 x 192 tiles with and without K splits)
+                     (65, 2048, 4096), (100, 11008, 4096), (128, 4096, 8200), (80, 6144, 9000), (97, 1024, 3000),
+                     (65, 8192, 16000), (90, 12288, 7000), (65, 1024, 32000), (128, 12288, 12000)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
