@@ -148,7 +148,7 @@ const char *ra_strerror(int code) {
 
 size_t ra_w8a16_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int x_dtype) {
   if (x_dtype != RA_F16 && x_dtype != RA_BF16) return 0;
-  if (M < 2 || M > 128) return 0;  // the row GEMV (M = 1) and the large-M tiled GEMM need none
+  if (M < 2 || M > kSplitTileMaxM) return 0;  // the row GEMV (M = 1) and the large-M tiled GEMM need none
   // The split-K kernel's plan (M <= 64; where it is not selected only a
   // forced RA_VARIANT_SPLITK launch uses it) or, at M = 33..128, the 64-row
   // tiles' split plan, whichever needs more (contiguous, aligned operands).

@@ -297,7 +297,7 @@ __device__ __forceinline__ int uniform_if(int v) {
   else return v;
 }
 
-// SPLIT (M <= 128, one or two rows of tiles): K is split over nsplit workgroups per
+// SPLIT (M <= 256, up to four rows of tiles): K is split over nsplit workgroups per
 // tile, ksplit K tiles each (the last may have fewer); workgroup b runs split
 // b % nsplit of tile b / nsplit. With nsplit > 1 each writes its fp32 sums
 // to the workspace with device-scope stores, waits for them and counts
@@ -747,10 +747,9 @@ bool tiled_small_selected(const GemmArgs &a) {
          a.K % tiled::BK == 0 && tiled_supported(a) && dma_span_ok(false, a.ldx, a.ldw, a.N, a.K, 256);
 }
 
-// M = 65..128: the large tiles leave most CUs idle where N is small (M=128
-// K=11008 N=4096: 16 tiles of 256 x 256), so these run two rows of the 64-row
-// split tiles too.
-constexpr int64_t kSplitTileMaxM = 128;
+// M = 65..256: the large tiles leave most CUs idle where N is small (M=128
+// K=11008 N=4096: 16 tiles of 256 x 256), so these run the split tiles too
+// (64 or 128 rows each; up to M = kSplitTileMaxM).
 
 static bool tiled_split_eligible(const GemmArgs &a) {
   if (tiled_small_selected(a)) return true;
@@ -775,8 +774,8 @@ static int device_cus();
 constexpr double kTileUs[4] = {0.0, 6.0, 10.0, 12.0};  // a_bnb
 constexpr double kTileUsPerMB = 16.0;
 constexpr double kTileCombineUs = 2.0;
-// M = 65..128 (two rows of 64-row tiles, or one row of 128-row tiles, bmb =
-// 2): the same form refitted (least squares on relative error) to the
+// M = 65..256 (rows of 64-row tiles, or of 128-row tiles, bmb = 2): the
+// same form refitted (least squares on relative error) to the
 // same-run times of all 24 (bmb, bnb, nsplit) at M = 65 / 96 / 128 over 7
 // (K, N) from K=2048 N=8192 to K=28672 N=8192: a = 1.9 / 7.9 / 10.3 us for
 // bmb = 1 and 5.8 / 12.3 / 18.6 for bmb = 2 (bnb = 1 / 2 / 3), 18.8 us per
@@ -791,11 +790,17 @@ constexpr double kTile2CombineUs = 4.5;
 extern int g_tiled_split;  // tuning builds: -1 never split, 10*bnb + nsplit forced
 #endif
 
+static int64_t large_tile_count(int64_t M, int64_t N, int cus);
+
 TiledSplitPlan tiled_split_plan(const GemmArgs &a) {
   TiledSplitPlan best{};
   if (!tiled_split_eligible(a)) return best;
   if ((uint64_t)((a.N - 1) * a.ldw + a.K) > DMA_SPAN) return best;  // one launch covers all of W
   const int cus = device_cus();
+  // M = 129..256: the large tiles where they fill at least half of the CUs
+  // (M=256 K=4096 N=28672, 224 tiles of 256 x 128: 59.7 us against 75.1 for
+  // the split plan; N=13824, 108 tiles: 59.0 against 49.0).
+  if (a.M > 2 * kSmallTileMaxM && 2 * large_tile_count(a.M, a.N, cus) >= cus) return best;
   const int64_t KT = a.K / tiled::BK;
   const int64_t tiles_m = (a.M + 63) / 64;
   auto cost = [&](int bmb, int bnb, int nsplit, int64_t ksplit) {
@@ -909,6 +914,11 @@ static DmaShape pick_dma_shape(int64_t M, int64_t N, bool gu, int cus) {
     if (first || t < best_t) best = c, best_t = t, first = false;
   }
   return best;
+}
+
+static int64_t large_tile_count(int64_t M, int64_t N, int cus) {
+  const DmaShape c = pick_dma_shape(M, N, false, cus);
+  return ((M + c.bm() - 1) / c.bm()) * ((N + c.bn() - 1) / c.bn());
 }
 
 static int device_cus() {
