@@ -87,7 +87,7 @@ int ra_w8a16_gemm(const void *x, int64_t ldx, int x_dtype,
 
 /*
  * ra_w8a16_gemm with a caller-owned device workspace, which lets the small-
- * batch kernels (2 <= M <= 256) split K over several workgroups and combine
+ * batch kernels (2 <= M <= 1024) split K over several workgroups and combine
  * their fp32 partial sums there in a fixed order (deterministic). Same
  * parity as ra_w8a16_gemm; it replaces the same reference call.
  * workspace_bytes must be at least ra_w8a16_gemm_workspace_size(M, N, K,

@@ -42,7 +42,7 @@ bool tiled_small_selected(const GemmArgs &a);
 hipError_t tiled_launch(const GemmArgs &a, hipStream_t s);
 // M = 33..64 (where tiled_small_selected): the small tile with K split over
 // workgroups, when the plan beats the 64 x 64 tile over all of K; M =
-// 65..256: rows of these tiles or of 128-row tiles, the best plan (above
+// 65..1024: rows of these tiles or of 128-row tiles, the best plan (above
 // M = 128 only where the large tiles fill less than half of the CUs).
 // nsplit > 1 needs ws_bytes of workspace, laid out as the split-K kernel's:
 // the counter block first. tiled_launch_ws runs it when it applies and the
@@ -53,7 +53,7 @@ struct TiledSplitPlan {
   size_t ws_bytes = 0;
 };
 TiledSplitPlan tiled_split_plan(const GemmArgs &a);
-constexpr int64_t kSplitTileMaxM = 256;  // largest M the split plans run
+constexpr int64_t kSplitTileMaxM = 1024;  // largest M the split plans run
 hipError_t tiled_launch_ws(const GemmArgs &a, void *ws, size_t ws_bytes, hipStream_t s);
 
 // Generic kernel: any shape, alignment and activation dtype.

@@ -297,7 +297,7 @@ __device__ __forceinline__ int uniform_if(int v) {
   else return v;
 }
 
-// SPLIT (M <= 256, up to four rows of tiles): K is split over nsplit workgroups per
+// SPLIT (M <= 1024, one or more rows of tiles): K is split over nsplit workgroups per
 // tile, ksplit K tiles each (the last may have fewer); workgroup b runs split
 // b % nsplit of tile b / nsplit. With nsplit > 1 each writes its fp32 sums
 // to the workspace with device-scope stores, waits for them and counts
@@ -747,14 +747,15 @@ bool tiled_small_selected(const GemmArgs &a) {
          a.K % tiled::BK == 0 && tiled_supported(a) && dma_span_ok(false, a.ldx, a.ldw, a.N, a.K, 256);
 }
 
-// M = 65..256: the large tiles leave most CUs idle where N is small (M=128
+// M = 65..1024: the large tiles leave most CUs idle where N is small (M=128
 // K=11008 N=4096: 16 tiles of 256 x 256), so these run the split tiles too
 // (64 or 128 rows each; up to M = kSplitTileMaxM).
 
 static bool tiled_split_eligible(const GemmArgs &a) {
   if (tiled_small_selected(a)) return true;
+  // One launch covers all rows of x (its copies' 31-bit offsets).
   return a.M > kSmallTileMaxM && a.M <= kSplitTileMaxM && a.K > 0 && a.K % tiled::BK == 0 &&
-         tiled_supported(a) && dma_span_ok(false, a.ldx, a.ldw, a.N, a.K, 256);
+         tiled_supported(a) && dma_span_ok(false, a.ldx, a.ldw, a.N, a.K, (int)std::max<int64_t>(a.M, 256));
 }
 
 static int device_cus();
@@ -797,10 +798,25 @@ TiledSplitPlan tiled_split_plan(const GemmArgs &a) {
   if (!tiled_split_eligible(a)) return best;
   if ((uint64_t)((a.N - 1) * a.ldw + a.K) > DMA_SPAN) return best;  // one launch covers all of W
   const int cus = device_cus();
-  // M = 129..256: the large tiles where they fill at least half of the CUs
-  // (M=256 K=4096 N=28672, 224 tiles of 256 x 128: 59.7 us against 75.1 for
-  // the split plan; N=13824, 108 tiles: 59.0 against 49.0).
-  if (a.M > 2 * kSmallTileMaxM && 2 * large_tile_count(a.M, a.N, cus) >= cus) return best;
+  // M > 128: the large tiles where they fill at least half of the CUs, and
+  // at M = 257..384 where they fill a whole round or N > 16384 (same-run
+  // times, bf16; M=320 K=4096 N=28672, 224 tiles of 192 x 256: 99.1 us
+  // against 118.2 for the split plan;
+  // M=256 K=4096 N=28672, 224 tiles of 256 x 128: 59.8 us against 61.2 for
+  // the split plan, N=13824, 108 tiles: 58.7 against 45.5; M=384 K=8192
+  // N=8192, 128 tiles: 90.8 against 64.8, K=28672 N=8192 271.6 against
+  // 220.0, K=5120 N=13824, 216 tiles: 78.0 against 61.9; M=512 K=5120
+  // N=13824, 216 tiles: 67.8 against 89.4; M=768: the large tiles ahead at
+  // every N >= 8192 measured).
+  bool guard = true;
+#ifdef RA_TUNING
+  guard = g_tiled_split != -2;  // tuning builds: -2 plans past this rule
+#endif
+  if (guard && a.M > 2 * kSmallTileMaxM) {
+    const int64_t lt = large_tile_count(a.M, a.N, cus);
+    const bool mid = a.M > 4 * kSmallTileMaxM && a.M <= 6 * kSmallTileMaxM;
+    if (mid ? (lt >= cus || a.N > 16384) : 2 * lt >= cus) return best;
+  }
   const int64_t KT = a.K / tiled::BK;
   const int64_t tiles_m = (a.M + 63) / 64;
   auto cost = [&](int bmb, int bnb, int nsplit, int64_t ksplit) {
@@ -817,7 +833,7 @@ TiledSplitPlan tiled_split_plan(const GemmArgs &a) {
   double best_t = one_row ? cost(1, 1, 1, KT) : 0.0;
   int force = 0;
 #ifdef RA_TUNING
-  force = g_tiled_split;
+  force = g_tiled_split == -2 ? 0 : g_tiled_split;
   if (force < 0) return best;
 #endif
   for (int bmb = 1; bmb <= kMaxTileBmb; ++bmb) {

@@ -105,16 +105,17 @@ def test_workspace_of_the_tiled_split_plan():
     assert lib.ra_w8a16_gemm_workspace_size(64, 8192, 11008, 0) >= 16384 + 64 * 4 * 32768
     assert lib.ra_w8a16_gemm_workspace_size(2048, 11008, 4096, 0) == 0
     assert lib.ra_w8a16_gemm_workspace_size(1, 11008, 4096, 0) == 0
-    # M = 65..256: the split plans of 64- and 128-row tiles; at K=11008 N=4096
+    # M = 65..1024: the split plans of 64- and 128-row tiles; at K=11008 N=4096
     # they split K, so they ask for a workspace; above M = 128 only where the
-    # large tiles fill less than half of the CUs (K=4096 N=28672: 224 tiles of
-    # 256 x 128 at M=256); from M = 257 none
+    # large tiles leave CUs idle (K=4096 N=28672: 224 tiles of 256 x 128 at
+    # M=256); from M = 1025 none
     assert lib.ra_w8a16_gemm_select(128, 4096, 11008, 0) == 2
     assert lib.ra_w8a16_gemm_workspace_size(128, 4096, 11008, 0) > 16384
     assert lib.ra_w8a16_gemm_workspace_size(65, 4096, 11008, 0) > 16384
     assert lib.ra_w8a16_gemm_workspace_size(256, 4096, 11008, 0) > 16384
+    assert lib.ra_w8a16_gemm_workspace_size(512, 4096, 11008, 0) > 16384
     assert lib.ra_w8a16_gemm_workspace_size(256, 28672, 4096, 0) == 0
-    assert lib.ra_w8a16_gemm_workspace_size(257, 4096, 11008, 0) == 0
+    assert lib.ra_w8a16_gemm_workspace_size(1025, 4096, 11008, 0) == 0
 
 
 def test_w8a8_argument_checks_without_device_work():

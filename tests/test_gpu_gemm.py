@@ -190,8 +190,9 @@ SPLIT_TILE_SHAPES = [(33, 9216, 8192), (64, 8192, 9000), (50, 6144, 12000), (64,
                      # and N; 128 x 128 and 128 x 192 tiles with and without K splits)
                      (65, 2048, 4096), (100, 11008, 4096), (128, 4096, 8200), (80, 6144, 9000), (97, 1024, 3000),
                      (65, 8192, 16000), (90, 12288, 7000), (65, 1024, 32000), (128, 12288, 12000),
-                     # M = 129..256, where the large tiles fill less than half of the CUs
-                     (129, 8192, 5000), (200, 4096, 4096), (256, 2048, 8192), (250, 11008, 4100)]
+                     # M = 129..1024, where the large tiles leave CUs idle
+                     (129, 8192, 5000), (200, 4096, 4096), (256, 2048, 8192), (250, 11008, 4100),
+                     (300, 2048, 8192), (384, 8192, 8200), (700, 4096, 4096), (1000, 2048, 4000)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
