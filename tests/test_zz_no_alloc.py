@@ -24,12 +24,13 @@ def test_noalloc_matches_workspace_entry_point(gpu):
     lib = _backend.load()
     stream = torch.cuda.current_stream(gpu).cuda_stream
     # (M, K, N, seed): the MLP's down projection at M=17, then a smaller split-K
-    # problem, then the 64-row tiles with K split over four workgroups
-    for (M, K, N, seed) in [(17, 28672, 8192, 1), (5, 16384, 1000, 2), (64, 8192, 11008, 3)]:
+    # problem, then the 64-row tiles with K split over four workgroups, in one
+    # row and in two
+    for (M, K, N, seed) in [(17, 28672, 8192, 1), (5, 16384, 1000, 2), (64, 8192, 11008, 3), (128, 11008, 4096, 4)]:
         print(f"  noalloc M={M} K={K} N={N}", flush=True)
         c = gemm_case(M, K, N, seed, device=gpu, dtype=torch.bfloat16, outlier_rows=True)
         xdt = _backend.dtype_code(c.x.dtype)
-        assert lib.ra_w8a16_gemm_select(M, N, K, xdt) == (_backend.VARIANT_TILED if M == 64 else
+        assert lib.ra_w8a16_gemm_select(M, N, K, xdt) == (_backend.VARIANT_TILED if M >= 64 else
                                                           _backend.VARIANT_SPLITK)
         need = lib.ra_w8a16_gemm_workspace_size(M, N, K, xdt)
         assert 0 < need <= 16 << 20
