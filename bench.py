@@ -10,7 +10,8 @@ Metric: int8_gemm HBM GB/s at M=1 and TFLOP/s at M=2048 (K=4096, N=11008).
   Infinity Cache) so every step streams its weight from HBM. ``value`` =
   algorithmic bytes per step (N*K + 4N + 2MK + 2MN) / (timed region / K).
 * ``steps``: exactly ``--steps`` launches are timed (whole graphs of 120
-  launches plus one graph of the remainder).
+  launches, the remainder launched from the host), queued behind an untimed
+  graph replay so that no launch latency falls inside the timed region.
 * ``config.python_int8_gemm_eager_us_per_call``: the Python ``int8_gemm``
   called eagerly in a host loop at the headline shape (argument checks,
   output allocation, C ABI call and launch), beside the graph-replay figure.
@@ -71,6 +72,9 @@ def parse():
                    default="all",
                    help="run one workload only (for profiler runs)")
     p.add_argument("--no-mlp", action="store_true", help="skip the fused-MLP timing")
+    p.add_argument("--mlp-rows", default="1,17,4096",
+                   help="with --only mlp: the MLP block's row counts to time (for profiler runs; any other "
+                        "value than the default also skips the RMSNorm and KV-codec lines)")
     p.add_argument("--shape", default="",
                    help="with --only shapes: time this one GEMM shape M,K,N instead (for profiler runs)")
     p.add_argument("--no-graph", action="store_true",
@@ -84,16 +88,17 @@ def parse():
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "hbm_traffic.md")
 
 
-def measured_traffic(workload: str, kernel: str):
-    """HBM bytes per launch of ``kernel`` on ``workload`` as measured by the
-    rocprofv3 FETCH_SIZE + WRITE_SIZE runs recorded in profiles/hbm_traffic.md
-    (table rows ``| workload | kernel | algorithmic B | fetch B | write B |
-    traffic B |``); None when no row matches."""
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the workload's kernel (per call of the MLP
+    block: its kernels summed) as measured by the rocprofv3 FETCH_SIZE +
+    WRITE_SIZE runs recorded in profiles/hbm_traffic.md (table rows
+    ``| workload | kernel | algorithmic B | fetch B | write B | traffic B |``);
+    None when no row matches."""
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
                 cells = [c.strip() for c in line.strip().strip("|").split("|")]
-                if len(cells) >= 6 and cells[0] == workload and cells[1] == kernel:
+                if len(cells) >= 6 and cells[0] == workload:
                     return int(cells[5].replace(",", ""))
     except (OSError, ValueError):
         pass
@@ -162,13 +167,23 @@ def time_eager(launcher, steps: int, warmup: int):
     return start.elapsed_time(end) / steps
 
 
+GRAPH_LATENCY: dict = {}   # per_graph -> launch latency of one graph replay (us), last measured
+
+
 def time_graph(launcher, steps: int, warmup: int, per_graph: int, warm_seconds: float = 0.2):
-    """Exactly ``steps`` launches, timed as HIP graph replays: a graph of
-    ``per_graph`` launches replayed steps // per_graph times, then a graph of
-    the remaining steps % per_graph launches; HIP events on the launch
-    stream bracket the timed replays. Untimed replays run for at least
-    ``warmup`` launches and ``warm_seconds`` first, so that the timed region
-    starts at steady clocks. Returns (ms per step, steps timed)."""
+    """Exactly ``steps`` launches timed with HIP events on the launch stream,
+    back to back on the GPU: steps // per_graph replays of a HIP graph of
+    ``per_graph`` launches, then the remaining steps % per_graph launches
+    issued from the host, all enqueued behind one untimed replay of the graph
+    that was enqueued just before the start event. That replay keeps the GPU
+    busy while the host enqueues the timed work, so no launch latency (host
+    launch, or the fixed cost of starting a graph, ~5-8 us on ROCm) falls
+    inside the timed region, which would otherwise be a visible share of it
+    with few steps. Untimed replays run for at least ``warmup`` launches and
+    ``warm_seconds`` first, so that the timed region starts at steady clocks.
+    The launch latency of one graph replay from an idle stream (minus
+    ``per_graph`` steady steps) is left in GRAPH_LATENCY[per_graph] (us).
+    Returns (ms per step, steps timed)."""
     import torch
     steps = max(1, steps)
     full, rem = divmod(steps, per_graph)
@@ -178,32 +193,37 @@ def time_graph(launcher, steps: int, warmup: int, per_graph: int, warm_seconds: 
         launcher.run(2)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    graph = rest = None
-    if full:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            launcher.run(per_graph)
-    if rem:
-        rest = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(rest):
-            launcher.run(rem)
-    warm = graph or rest
-    warm_n = per_graph if graph is not None else rem
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launcher.run(per_graph)
     t0, done = time.perf_counter(), 0
     while done < warmup or time.perf_counter() - t0 < warm_seconds:
-        warm.replay()
+        graph.replay()
         torch.cuda.synchronize()
-        done += warm_n
+        done += per_graph
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    graph.replay()                # untimed head start, not waited for
     start.record()
     for _ in range(full):
         graph.replay()
-    if rest is not None:
-        rest.replay()
+    if rem:
+        launcher.run(rem)
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps, steps
+    ms = start.elapsed_time(end) / steps
+    # launch latency of one replay from an idle stream
+    lat = []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        graph.replay()
+        s1.record()
+        torch.cuda.synchronize()
+        lat.append(s0.elapsed_time(s1) - per_graph * ms)
+    GRAPH_LATENCY[per_graph] = round(sorted(lat)[1] * 1e3, 2)
+    return ms, steps
 
 
 def time_python_int8_gemm(x, copies, scale, steps: int, warmup: int):
@@ -223,6 +243,27 @@ def time_python_int8_gemm(x, copies, scale, steps: int, warmup: int):
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
+
+
+def host_info():
+    """CPU model, torch version and the BLAS / oneDNN backends the CPU
+    fallback's F.linear dispatches to (torch.__config__)."""
+    import torch
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    cfg = torch.__config__.show()
+    blas = next((ln.split("=", 1)[1].strip() for ln in cfg.splitlines() if "BLAS_INFO=" in ln), "unknown")
+    blas = blas.split(",")[0]
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "torch": torch.__version__,
+            "blas": blas, "mkl": torch.backends.mkl.is_available(),
+            "mkldnn": torch.backends.mkldnn.is_available()}
 
 
 def cpu_baseline(M, K, N, seed, budget_s):
@@ -269,7 +310,7 @@ def cpu_baseline_prefill(budget_s, rows=64):
     times.sort()
     med = times[len(times) // 2]
     return {"value": round(gemm_flops(rows, Kp, Np) / med / 1e12, 4), "unit": "TFLOP/s",
-            "cores": torch.get_num_threads(), "kind": "port",
+            "cores": torch.get_num_threads(), "kind": "port", **host_info(),
             "sample": f"{len(times)} calls of the reference fallback on the first {rows} rows of the M={Mp} "
                       f"K={Kp} N={Np} fp16 workload (weights dequantised per call), median "
                       f"{med * 1e3:.1f} ms/call"}
@@ -302,7 +343,7 @@ def cpu_baseline_mlp(budget_s):
     times.sort()
     med = times[len(times) // 2]
     return {"value": round(mlp_bytes(1, H, I) / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "kind": "port", **host_info(),
             "sample": f"{len(times)} calls of the reference MLP composition (weights dequantised per call) at "
                       f"M=1 H={H} I={I} bf16, median {med * 1e3:.1f} ms/call"}
 
@@ -478,14 +519,41 @@ def run_shapes(args, dev):
         gbs = gemm_bytes(M, K, N) / (ms * 1e-3) / 1e9
         variant = _backend.load().ra_w8a16_gemm_select(M, N, K, _backend.F16)
         rec = {"group": group, "M": M, "K": K, "N": N, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-               "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "kernel_variant": VARIANT_NAMES.get(variant, str(variant))}
+               "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "kernel_variant": VARIANT_NAMES.get(variant, str(variant)),
+               "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                            "frac": round(gbs / PEAK_HBM_GBS, 4),
+                            "traffic": measured_traffic(f"{group} M={M} K={K} N={N}")}}
         rows.append(rec)
         log(f"{group} M={M} K={K} N={N}: {rec['us']} us, {rec['GB/s']} GB/s ({rec['frac_hbm']:.1%} of HBM peak)")
         del copies, launcher, c, y
     return rows
 
 
-PROBE_LIB = os.path.join(HERE, "rotalabs-accel_amd", "rotalabs_accel", "_lib", "librotaccel_probe.so")
+PROBE_SRC = os.path.join(HERE, "bench_probe.hip")
+PROBE_LIB = os.path.join(HERE, "bench_probe.so")
+
+
+def build_probe(force: bool = False) -> str:
+    """Compile the measurement probe (bench_probe.hip, a plain streaming read
+    with the decode kernels' access pattern; not part of the library) into
+    bench_probe.so with the library's hipcc flags, unless a build newer than
+    the source exists. Returns the library path."""
+    if (not force and os.path.exists(PROBE_LIB)
+            and os.path.getmtime(PROBE_LIB) >= os.path.getmtime(PROBE_SRC)):
+        return PROBE_LIB
+    import importlib.util
+    import subprocess
+    spec = importlib.util.spec_from_file_location(
+        "rotalabs_accel_build", os.path.join(HERE, "rotalabs-accel_amd", "rotalabs_accel", "_build.py"))
+    bld = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bld)
+    tmp = PROBE_LIB + ".tmp"
+    res = subprocess.run([bld._hipcc(), *bld.compile_flags(), "-shared", PROBE_SRC, "-o", tmp],
+                         capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {PROBE_SRC}:\n{res.stderr}")
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
 
 
 def run_read_ceiling(args, dev):
@@ -499,7 +567,7 @@ def run_read_ceiling(args, dev):
     import ctypes
     import torch
     from workloads import gemm_bytes, gemm_case
-    lib = ctypes.CDLL(PROBE_LIB)
+    lib = ctypes.CDLL(build_probe())
     lib.rap_stream_rows.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
                                     ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                     ctypes.c_void_p]
@@ -553,30 +621,39 @@ def run_mlp(args, dev):
     q_gu, s_gu = ra.quantize_weight_per_channel(torch.randn(2 * I, H, device=dev, generator=g) * 0.02)
     q_d, s_d = ra.quantize_weight_per_channel(torch.randn(H, I, device=dev, generator=g) * 0.02)
     out = {}
+    rows_wanted = {int(v) for v in args.mlp_rows.split(",")}
     for M, calls in ((1, 20), (17, 20), (4096, 3)):
         x = torch.randn(M, H, device=dev, generator=g).to(torch.bfloat16)
+        if M not in rows_wanted:
+            continue
 
         class _Step:
             def run(self, n):
                 for _ in range(n):
                     int8_mlp(x, norm_w, q_gu, s_gu, q_d, s_d)
-        ms, _ = time_graph(_Step(), calls * 3, calls, per_graph=calls)
+        if args.no_graph:
+            ms = time_eager(_Step(), calls * 3, calls)
+        else:
+            ms, _ = time_graph(_Step(), calls * 3, calls, per_graph=calls)
         rec = {"us_per_call": round(ms * 1e3, 2), "steps": calls * 3}
+        traffic = measured_traffic(f"mlp M={M} H={H} I={I}")
         if M <= 64:   # weight-streaming (HBM-bound) sizes
             gbs = mlp_bytes(M, H, I) / (ms * 1e-3) / 1e9
             rec.update({"GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                                     "traffic": None}})
+                                     "traffic": traffic}})
         else:
             tf = mlp_flops(M, H, I) / (ms * 1e-3) / 1e12
             rec.update({"TFLOP/s": round(tf, 1), "frac_mfma": round(tf / PEAK_FP16_TFLOPS, 4),
                         "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_FP16_TFLOPS,
                                      "unit": "TFLOP/s", "frac": round(tf / PEAK_FP16_TFLOPS, 4),
-                                     "traffic": None}})
+                                     "traffic": traffic}})
         out[f"M={M}"] = rec
         log(f"mlp M={M} H={H} I={I} bf16: {rec}")
         del x
+    if args.mlp_rows != "1,17,4096":
+        return out
     # RMSNorm of x + residual (the block's prologue in a decoder layer), HBM-bound:
     # reads x, residual, weight, writes y; 3 input sets (384 MiB) cycled so the
     # reads come from HBM, not the 256 MB Infinity Cache.
@@ -656,7 +733,7 @@ def main():
     Ml, Kl, Nl, _ = PREFILL_LARGE
     lms = ltflops = float("nan")
     lvariant = None
-    if args.only in ("all", "prefill", "prefill_large"):
+    if args.only in ("all", "prefill_large"):
         lms, ltflops, lvariant = run_prefill(args, dev, PREFILL_LARGE)
     w8a8 = None
     if args.only in ("all", "w8a8"):
@@ -705,16 +782,21 @@ def main():
             "bytes_per_step": dbytes,
             "kernel_variant": VARIANT_NAMES.get(variant, str(variant)),
             "timing": ("host-launched loop" if args.no_graph else
-                       "HIP graph of 120 launches replayed") + "; HIP events on the launch stream",
+                       f"{timed_steps // (10 * N_COPIES)} replays of a HIP graph of {10 * N_COPIES} launches and "
+                       f"{timed_steps % (10 * N_COPIES)} host-launched C ABI calls, all queued behind an untimed "
+                       "graph replay enqueued just before the start event") + "; HIP events on the launch stream",
+            "graph_launch_latency_us": GRAPH_LATENCY.get(10 * N_COPIES),
             "host_launched_us_per_step": round(ms_eager * 1e3, 3),
             "python_int8_gemm_eager_us_per_call": round(ms_py * 1e3, 3),
-            "steps_note": "steps = launches timed, exactly --steps (whole 120-launch graphs plus one graph "
-                          "of the remainder)",
+            "steps_note": f"steps = launches timed, exactly --steps (whole {10 * N_COPIES}-launch graphs plus "
+                          "the remainder launched from the host); graph_launch_latency_us = one replay of a "
+                          f"{10 * N_COPIES}-launch graph from an idle stream minus {10 * N_COPIES} steady steps, "
+                          "kept out of the timed region",
         },
         "roofline": {
             "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(gbs / PEAK_HBM_GBS, 4),
-            "traffic": measured_traffic(f"decode M={M} K={K} N={N}", VARIANT_KERNELS.get(variant, "")),
+            "traffic": measured_traffic(f"decode M={M} K={K} N={N}"),
         },
         "prefill": {
             "metric": "int8_gemm TFLOP/s @M=2048 K=4096 N=11008",
@@ -722,8 +804,7 @@ def main():
             "kernel_variant": VARIANT_NAMES.get(pvariant, str(pvariant)),
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_FP16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
-                         "traffic": measured_traffic(f"prefill M={Mp} K={Kp} N={Np}",
-                                                     VARIANT_KERNELS.get(pvariant, ""))},
+                         "traffic": measured_traffic(f"prefill M={Mp} K={Kp} N={Np}")},
         },
         "prefill_large": {
             "metric": f"int8_gemm TFLOP/s @M={Ml} K={Kl} N={Nl}",
@@ -731,8 +812,7 @@ def main():
             "kernel_variant": VARIANT_NAMES.get(lvariant, str(lvariant)),
             "roofline": {"bound": "mfma", "achieved": round(ltflops, 1), "peak": PEAK_FP16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(ltflops / PEAK_FP16_TFLOPS, 4),
-                         "traffic": measured_traffic(f"prefill M={Ml} K={Kl} N={Nl}",
-                                                     VARIANT_KERNELS.get(lvariant, ""))},
+                         "traffic": measured_traffic(f"prefill M={Ml} K={Kl} N={Nl}")},
         },
     }
     if shapes is not None:
@@ -756,7 +836,7 @@ def main():
         out["mlp"]["cpu_baseline"] = cpu_mlp
     if cpu is not None:
         out["cpu_baseline"] = {
-            "value": round(cpu["gbs"], 3), "unit": "GB/s", "cores": cpu["threads"], "kind": "port",
+            "value": round(cpu["gbs"], 3), "unit": "GB/s", "cores": cpu["threads"], "kind": "port", **host_info(),
             "sample": f"{cpu['calls']} calls of the reference fallback (dequantize + F.linear) at "
                       f"M={M} K={K} N={N} fp16 on the host CPU, median {cpu['med_s'] * 1e3:.2f} ms/call",
         }

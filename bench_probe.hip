@@ -10,7 +10,8 @@
 //    each wave stores one 16-bit word y[n] -- without the dequantisation and
 //    dot products.
 // Their durations are the single-launch floors the M=1 GEMV kernels are
-// compared with (bench.py --only ceiling). Built into librotaccel_probe.so.
+// compared with (bench.py --only ceiling). bench.py builds it into
+// bench_probe.so beside itself, with the library's compile flags.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 

@@ -25,7 +25,14 @@
 extern "C" {
 #endif
 
-#define RA_ABI_VERSION 6
+#define RA_ABI_VERSION 7
+
+/* Caller workspaces (ra_w8a16_gemm_ws, ra_w8a16_gateup_swiglu_ws) start on
+ * this byte boundary (RA_ERR_ARG otherwise). Their first
+ * RA_WORKSPACE_COUNTER_BYTES bytes are the counter block, which must be zero
+ * before the first use; the rest needs no initialisation. */
+#define RA_WORKSPACE_ALIGN 256
+#define RA_WORKSPACE_COUNTER_BYTES 16384
 
 enum ra_dtype { RA_F16 = 0, RA_BF16 = 1, RA_F32 = 2 };
 
@@ -93,9 +100,14 @@ int ra_w8a16_gemm(const void *x, int64_t ldx, int x_dtype,
  * workspace_bytes must be at least ra_w8a16_gemm_workspace_size(M, N, K,
  * x_dtype) (RA_ERR_WORKSPACE otherwise); workspace may be NULL (or the size
  * 0), which runs the kernels that need none, as ra_w8a16_gemm does.
- * The workspace must be zero-filled before its first use; every call leaves
- * it ready for the next one (its counters back at zero). Calls that may run
- * concurrently (other streams) need workspaces of their own.
+ * The workspace starts on an RA_WORKSPACE_ALIGN boundary (RA_ERR_ARG
+ * otherwise). Its counter block (the first RA_WORKSPACE_COUNTER_BYTES) must
+ * be zero before its first use; every call leaves it ready for the next one
+ * (its counters back at zero). Calls that may run concurrently (other
+ * streams, graphs replayed on other streams) need workspaces of their own.
+ * Under HIP graph capture a call records the workspace's address: keep the
+ * buffer alive, and its counter block zero before each replay, for as long
+ * as the graph may be replayed.
  */
 int ra_w8a16_gemm_ws(const void *x, int64_t ldx, int x_dtype,
                      const int8_t *w, int64_t ldw, const float *scale,
@@ -164,6 +176,16 @@ int ra_w8a16_gateup_swiglu_ws(const void *x, int64_t ldx, int x_dtype,
                               void *workspace, size_t workspace_bytes, void *stream);
 
 size_t ra_w8a16_gateup_workspace_size(int64_t M, int64_t I, int64_t K, int x_dtype);
+
+/*
+ * Whether `stream` is being captured into a HIP graph (*capturing = 1, and
+ * *capture_id = the capture's id, unique within the process) or not
+ * (*capturing = 0, *capture_id = 0). Host plumbing with no counterpart in the
+ * reference: the Python layer gives every graph capture a workspace of its
+ * own, so that graphs never share one and a replay never depends on state
+ * another graph or an eager call left behind.
+ */
+int ra_stream_capture_info(void *stream, int *capturing, unsigned long long *capture_id);
 
 /*
  * y[r,:] = (x[r,:] * rsqrt(mean(x[r,:]^2) + eps)) rounded to x_dtype, times

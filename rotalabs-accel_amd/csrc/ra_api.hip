@@ -71,8 +71,11 @@ int select_variant(const GemmArgs &a, bool have_ws) {
   // Split K: long K, or from 16 rows K >= 11008 over at most 4096 weight
   // rows (M=64 K=14336 N=4096: 29.1 us against 55.0 for the small-batch
   // kernel, M=16 K=11008 N=4096 15.0 against 16.3).
+  // Only where the plan does split (S > 1): with S = 1 the problem needs no
+  // workspace, and a call with one must run what a call without one runs.
   if (have_ws && a.M <= kSkinnyMaxM && splitk_supported(a) &&
-      (a.K >= kSplitkMinK || (a.M >= 16 && a.K >= 11008 && a.N <= 4096)))
+      (a.K >= kSplitkMinK || (a.M >= 16 && a.K >= 11008 && a.N <= 4096)) &&
+      splitk_plan(a.M, a.N, a.K, false, true).S > 1)
     return RA_VARIANT_SPLITK;
   // M = 3..64: the small-batch kernel (line-wide weight loads, activations
   // read once per 48 rows) where K % 128 == 0, else the split-K MFMA kernel;
@@ -83,6 +86,13 @@ int select_variant(const GemmArgs &a, bool have_ws) {
   if (tiled_supported(a)) return RA_VARIANT_TILED;
   if (skinny_supported(a)) return RA_VARIANT_SKINNY;
   return RA_VARIANT_GENERIC;
+}
+
+// A caller workspace must start on an RA_WORKSPACE_ALIGN boundary (the
+// kernels use 4-byte atomics on its counters and 16-byte stores and loads of
+// its partial sums).
+bool ws_misaligned(const void *ws, size_t bytes) {
+  return ws != nullptr && bytes > 0 && reinterpret_cast<uintptr_t>(ws) % RA_WORKSPACE_ALIGN != 0;
 }
 
 int check_gemm(const GemmArgs &a) {
@@ -166,6 +176,7 @@ int ra_w8a16_gemm_ex(const void *x, int64_t ldx, int x_dtype, const int8_t *w, i
   const GemmArgs a{x, ldx, x_dtype, w, ldw, scale, bias, bias_dtype, y, ldy, M, N, K};
   int st = check_gemm(a);
   if (st != RA_OK) return st;
+  if (ws_misaligned(workspace, workspace_bytes)) return RA_ERR_ARG;
   if (M == 0 || N == 0) return RA_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool have_ws = workspace != nullptr && workspace_bytes > 0;
@@ -226,7 +237,8 @@ int ra_w8a16_gemm_select(int64_t M, int64_t N, int64_t K, int x_dtype) {
 
 size_t ra_w8a16_gateup_workspace_size(int64_t M, int64_t I, int64_t K, int x_dtype) {
   if (x_dtype != RA_F16 && x_dtype != RA_BF16) return 0;
-  if (M < 2 || M > kSkinnyMaxM) return 0;
+  // Only the split-K gate/up kernel uses a workspace, from K = kSplitkMinK.
+  if (M < 2 || M > kSkinnyMaxM || K < kSplitkMinK) return 0;
   const SplitkPlan p = splitk_plan(M, I, K, true, true);
   return p.ok ? p.ws_bytes : 0;
 }
@@ -245,6 +257,7 @@ int ra_w8a16_gateup_swiglu_ws(const void *x, int64_t ldx, int x_dtype, const int
   if (M == 0 || I == 0) return RA_OK;
   if (!h || !w || !scale || (K > 0 && !x)) return RA_ERR_ARG;
   if (ldx < K || ldw < K || ldh < I) return RA_ERR_ARG;
+  if (ws_misaligned(workspace, workspace_bytes)) return RA_ERR_ARG;
   const GateUpArgs a{x, ldx, x_dtype, w, ldw, scale, h, ldh, M, I, K};
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool have_ws = workspace != nullptr && workspace_bytes > 0;
@@ -262,6 +275,16 @@ int ra_w8a16_gateup_swiglu_ws(const void *x, int64_t ldx, int x_dtype, const int
   if (K > 0 && gateup_gemv_supported(a)) return to_status(gateup_gemv_launch(a, s));
   if (K > 0 && gateup_tiled_supported(a)) return to_status(gateup_tiled_launch(a, s));
   return to_status(gateup_generic_launch(a, s));
+}
+
+int ra_stream_capture_info(void *stream, int *capturing, unsigned long long *capture_id) {
+  if (!capturing || !capture_id) return RA_ERR_ARG;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  unsigned long long id = 0;
+  if (hipStreamGetCaptureInfo(static_cast<hipStream_t>(stream), &st, &id) != hipSuccess) return RA_ERR_DEVICE;
+  *capturing = st == hipStreamCaptureStatusActive ? 1 : 0;
+  *capture_id = *capturing ? id : 0;
+  return RA_OK;
 }
 
 int ra_rmsnorm(const void *x, int64_t ldx, int x_dtype, const void *weight, int w_dtype, void *y, int64_t ldy,

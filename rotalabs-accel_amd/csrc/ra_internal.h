@@ -95,7 +95,7 @@ hipError_t gateup_batch_launch(const GateUpArgs &a, hipStream_t s);
 // ws_bytes (a zeroed counter block of cnt_bytes, then the partial sums).
 // Bytes of the counter block at the start of every split-K workspace (must
 // be zero before the first use; each call leaves it zero).
-constexpr size_t kSplitkCounterBytes = 4096 * sizeof(int);
+constexpr size_t kSplitkCounterBytes = RA_WORKSPACE_COUNTER_BYTES;  // 4096 counters
 struct SplitkPlan {
   bool ok;
   int mt, tw, S, kc, nb;

@@ -20,7 +20,11 @@ _lock = threading.Lock()
 _lib = None
 _load_error: str | None = None
 
-ABI_VERSION = 6
+ABI_VERSION = 7
+
+# include/rotaccel.h: workspace alignment and the bytes of its counter block
+WORKSPACE_ALIGN = 256
+WORKSPACE_COUNTER_BYTES = 16384
 
 # enum ra_dtype
 F16, BF16, F32 = 0, 1, 2
@@ -48,6 +52,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "ra_w8a16_gateup_swiglu_ws": ([p, i64, i32, p, i64, p, p, i64, i64, i64, i64, p, sz, p], i32),
         "ra_w8a16_gateup_workspace_size": ([i64, i64, i64, i32], sz),
         "ra_w8a16_gemm_select": ([i64, i64, i64, i32], i32),
+        "ra_stream_capture_info": ([p, ctypes.POINTER(i32), ctypes.POINTER(ctypes.c_ulonglong)], i32),
         "ra_w8a16_gateup_swiglu": ([p, i64, i32, p, i64, p, p, i64, i64, i64, i64, p], i32),
         "ra_rmsnorm": ([p, i64, i32, p, i32, p, i64, i32, i64, i64, f32, p], i32),
         "ra_rmsnorm_residual": ([p, i64, i32, p, i64, i32, p, i32, p, i64, i32, i64, i64, f32, p], i32),
@@ -126,29 +131,65 @@ def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-_workspaces: dict = {}
+_workspaces: dict = {}   # (device, stream) -> buffer of the eager calls on that stream
+_captured: dict = {}     # (device, stream, capture id) -> buffer of one graph capture
+_held: list = []         # every buffer a captured graph may use: never released
 _WS_ROUND = 1 << 20
 
 
-def workspace(device: torch.device, nbytes: int):
-    """(pointer, bytes) of a zero-filled device workspace of at least
-    ``nbytes`` for launches on torch's current stream of ``device``, or
-    (None, 0) when ``nbytes`` is 0.
+def capture_info(stream: int) -> tuple[bool, int]:
+    """(capturing, capture id) of a hipStream_t (the id is 0 when not capturing)."""
+    cap, cid = ctypes.c_int(0), ctypes.c_ulonglong(0)
+    check(load().ra_stream_capture_info(stream, ctypes.byref(cap), ctypes.byref(cid)))
+    return bool(cap.value), int(cid.value)
 
-    The kernels that use a workspace leave it as they found it (their
-    counters back at zero), so one buffer serves every call issued on a
-    stream; each stream gets its own, as calls on different streams may
-    overlap. The buffer comes from torch's allocator (also during graph
-    capture, where its zero fill is recorded as a kernel) and grows in 1 MiB
-    steps when a larger problem needs more."""
+
+def workspace(device: torch.device, nbytes: int):
+    """(pointer, bytes) of a device workspace of at least ``nbytes`` whose
+    counter block is zero when the next launch on torch's current stream of
+    ``device`` reads it, or (None, 0) when ``nbytes`` is 0.
+
+    The kernels that use a workspace leave its counters at zero, so one buffer
+    serves a sequence of calls that run one after another:
+
+    * Eager calls: one buffer per (device, stream), zero-filled when it is
+      allocated (calls on different streams may overlap, so each stream has
+      its own). A larger problem replaces it; the old buffer goes back to
+      torch's allocator, which reuses its memory only for work ordered after
+      the calls on that stream.
+    * Calls under HIP graph capture: one buffer per capture (and capturing
+      stream), allocated from the graph's memory pool when the capture first
+      needs it, with the fill of its counter block recorded into the graph
+      just before that call, so every replay clears the counters before the
+      first kernel reads them -- whatever ran before the replay (another
+      graph, eager calls) and whether or not this graph ever ran. Graphs never
+      share a buffer, and no buffer a graph was captured with is released
+      (they are held until the process ends), so a replay never reads memory
+      that was handed to another tensor.
+
+    Buffers are 256-byte aligned (torch's allocator aligns every block to at
+    least 512 bytes) and grow in 1 MiB steps."""
     if nbytes <= 0:
         return None, 0
-    key = (_device_index(device), stream_handle(device))
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        size = -(-nbytes // _WS_ROUND) * _WS_ROUND
-        ws = torch.zeros(size, dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
+    dev = _device_index(device)
+    stream = stream_handle(device)
+    capturing, cid = capture_info(stream)
+    size = -(-nbytes // _WS_ROUND) * _WS_ROUND
+    if not capturing:
+        key = (dev, stream)
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.zeros(size, dtype=torch.uint8, device=device)
+            _workspaces[key] = ws
+    else:
+        key = (dev, stream, cid)
+        ws = _captured.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(size, dtype=torch.uint8, device=device)
+            ws[:WORKSPACE_COUNTER_BYTES].zero_()  # a fill kernel, recorded into the graph
+            _captured[key] = ws
+            _held.append(ws)
+    assert ws.data_ptr() % WORKSPACE_ALIGN == 0
     return ws.data_ptr(), ws.numel()
 
 

@@ -33,8 +33,6 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 BUILD_DIR = os.path.join(PROJ_DIR, "_build")
 LIB_DIR = os.path.join(PKG_DIR, "_lib")
 LIB_PATH = os.path.join(LIB_DIR, "librotaccel.so")
-PROBE_SRC = os.path.join(CSRC, "probe", "ra_probe.hip")
-PROBE_LIB = os.path.join(LIB_DIR, "librotaccel_probe.so")   # bench.py --read-ceiling only
 
 ARCH = "gfx950"
 
@@ -89,12 +87,6 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH} from {len(sources)} sources")
-    # the measurement probe of bench.py (a plain streaming read; not part of the library)
-    tmp = PROBE_LIB + ".tmp"
-    res = subprocess.run([_hipcc(), *compile_flags(), "-shared", PROBE_SRC, "-o", tmp], capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {PROBE_SRC}:\n{res.stderr}")
-    os.replace(tmp, PROBE_LIB)
     return LIB_PATH
 
 

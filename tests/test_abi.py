@@ -61,7 +61,8 @@ def test_argument_checks_without_device_work():
     # before any launch
     need = lib.ra_w8a16_gemm_workspace_size(17, 8192, 28672, 0)
     assert need > 0
-    assert lib.ra_w8a16_gemm_ws(p, 28672, 0, p, 28672, p, n, 0, p, 8192, 17, 8192, 28672, p, need - 1, n) == 6
+    wsa = (p + 255) // 256 * 256   # workspaces start on a 256-byte boundary
+    assert lib.ra_w8a16_gemm_ws(p, 28672, 0, p, 28672, p, n, 0, p, 8192, 17, 8192, 28672, wsa, need - 1, n) == 6
     assert lib.ra_w8a16_gemm_workspace_size(1, 11008, 4096, 0) == 0      # row GEMV: none
     assert lib.ra_w8a16_gemm_workspace_size(2048, 11008, 4096, 0) == 0   # tiled: none
     assert lib.ra_w8a16_gateup_swiglu_ws(n, 0, 0, n, 0, n, n, 0, 0, 8, 8, n, 0, n) == 0
@@ -136,3 +137,58 @@ def test_w8a8_argument_checks_without_device_work():
     assert lib.ra_w8a8_gemm(p, 8, p, p, 16, p, n, 0, p, 16, 0, 4, 4, 16, n) == 1  # ldxq < K
     assert lib.ra_w8a8_gemm(p, 16, n, p, 16, p, n, 0, p, 16, 0, 4, 4, 16, n) == 1  # no x scales
     assert lib.ra_w8a8_gemm(p, 16, p, p, 16, p, n, 0, p, 16, 0, 4, 4, -16, n) == 1
+
+
+def test_workspace_constants_match_header():
+    src = open(HEADER).read()
+    assert int(re.search(r"#define RA_WORKSPACE_ALIGN (\d+)", src).group(1)) == _backend.WORKSPACE_ALIGN
+    assert int(re.search(r"#define RA_WORKSPACE_COUNTER_BYTES (\d+)", src).group(1)) == \
+        _backend.WORKSPACE_COUNTER_BYTES
+
+
+def test_misaligned_workspace_refused_before_any_launch():
+    """A workspace that does not start on a 256-byte boundary is RA_ERR_ARG
+    (the kernels do 4-byte atomics on its counters and 16-byte stores of its
+    partial sums), for the GEMM and the gate/up entry points alike; checked
+    before kernel selection, so no device work happens."""
+    lib = _backend.load()
+    n = None
+    buf = ctypes.create_string_buffer(4096)
+    base = (ctypes.addressof(buf) + 255) // 256 * 256
+    p = ctypes.addressof(buf)
+    need = lib.ra_w8a16_gemm_workspace_size(17, 8192, 28672, 1)
+    for off in (4, 16, 128):
+        assert lib.ra_w8a16_gemm_ws(p, 28672, 1, p, 28672, p, n, 0, p, 8192, 17, 8192, 28672,
+                                    base + off, need, n) == 1
+        assert lib.ra_w8a16_gemm_ex(p, 28672, 1, p, 28672, p, n, 0, p, 8192, 17, 8192, 28672, 7,
+                                    base + off, need, n) == 1
+        assert lib.ra_w8a16_gateup_swiglu_ws(p, 16384, 1, p, 16384, p, p, 3000, 17, 3000, 16384,
+                                             base + off, 1 << 30, n) == 1
+    # an aligned but too small workspace still reports RA_ERR_WORKSPACE
+    assert lib.ra_w8a16_gemm_ws(p, 28672, 1, p, 28672, p, n, 0, p, 8192, 17, 8192, 28672,
+                                base, need - 1, n) == 6
+
+
+def test_select_agrees_with_the_workspace_size():
+    """Where the split-K plan does not split (S = 1) the problem needs no
+    workspace, so the automatic selection must not pick the split-K kernel
+    either: a call with a workspace then runs what a call without one runs
+    (M=8 K=16384 N=65536, M=2 K=16384 N=128256). Where it does split, select
+    reports split K and the size is non-zero."""
+    lib = _backend.load()
+    for (M, N, K) in ((8, 65536, 16384), (2, 128256, 16384)):
+        assert lib.ra_w8a16_gemm_workspace_size(M, N, K, 1) == 0
+        assert lib.ra_w8a16_gemm_select(M, N, K, 1) != 7
+    for (M, N, K) in ((17, 8192, 28672), (8, 16384, 16384), (16, 4096, 11008)):
+        assert lib.ra_w8a16_gemm_select(M, N, K, 1) == 7
+        assert lib.ra_w8a16_gemm_workspace_size(M, N, K, 1) > _backend.WORKSPACE_COUNTER_BYTES
+
+
+def test_gateup_workspace_only_where_gateup_splits():
+    """The gate/up kernels split K only from K = 16384; below it the size is 0,
+    so the Python layer allocates no workspace it never uses."""
+    lib = _backend.load()
+    assert lib.ra_w8a16_gateup_workspace_size(17, 28672, 8192, 1) == 0
+    assert lib.ra_w8a16_gateup_workspace_size(17, 3000, 16384, 1) > _backend.WORKSPACE_COUNTER_BYTES
+    assert lib.ra_w8a16_gateup_workspace_size(1, 3000, 16384, 1) == 0
+
