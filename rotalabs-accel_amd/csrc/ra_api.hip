@@ -33,6 +33,11 @@ int g_w8a8_mode = 0;
 int g_rows_lds = 0;
 }
 #endif
+#ifdef RA_TRACE
+namespace ra {
+void *g_trace_buf = nullptr;
+}
+#endif
 
 namespace {
 
@@ -139,6 +144,10 @@ void ra_tune_sk(int s, int dmax) { ra::g_sk_s = s; ra::g_sk_dmax = dmax; }
 void ra_tune_tiled_split(int v) { ra::g_tiled_split = v; }
 void ra_tune_w8a8(int mode) { ra::g_w8a8_mode = mode; }
 void ra_tune_rows_lds(int v) { ra::g_rows_lds = v; }
+#endif
+#ifdef RA_TRACE
+// Trace builds only: device buffer for the tiled kernel's per-workgroup timestamps (NULL: none).
+void ra_tune_trace(void *buf) { ra::g_trace_buf = buf; }
 #endif
 
 int ra_abi_version(void) { return RA_ABI_VERSION; }

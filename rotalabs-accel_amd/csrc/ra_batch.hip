@@ -130,7 +130,7 @@ __global__ __launch_bounds__(NW * 64) void batch_kernel(const uint16_t *__restri
         const int chunk = 2 * s + (g >> 1);                                                         \
         const uint2 q = *reinterpret_cast<const uint2 *>(                                           \
             slot + row * KS + ((chunk ^ ((row >> 1) & 7)) << 4) + 8 * (g & 1));                     \
-        const uint4 a = A::dq8(q.x, q.y);                                                           \
+        const uint4 a = A::dq8s(q.x, q.y);                                                           \
         _Pragma("unroll") for (int mt = 0; mt < MT; ++mt) acc[t][mt] =                              \
             A::mfma16(a, xf[DP_][s][mt], acc[t][mt]);                                               \
       }                                                                                             \
@@ -313,10 +313,10 @@ __global__ __launch_bounds__(512) void batch_xlds_kernel(const uint16_t *__restr
       xf[j] = *reinterpret_cast<const uint4 *>(xrow + (((c0 + 16 * kst(s + rot) + j) ^ sw) << 4));
     const uint4 X = *reinterpret_cast<const uint4 *>(slot + xr_off + (((2 * g) ^ xsw) << 4));
     const uint4 Y = *reinterpret_cast<const uint4 *>(slot + xr_off + (((2 * g + 1) ^ xsw) << 4));
-    acc0 = A::mfma16(A::dq8(X.x, X.y), xf[0], acc0);
-    acc1 = A::mfma16(A::dq8(Y.x, Y.y), xf[2], acc1);
-    acc0 = A::mfma16(A::dq8(X.z, X.w), xf[1], acc0);
-    acc1 = A::mfma16(A::dq8(Y.z, Y.w), xf[3], acc1);
+    acc0 = A::mfma16(A::dq8s(X.x, X.y), xf[0], acc0);
+    acc1 = A::mfma16(A::dq8s(Y.x, Y.y), xf[2], acc1);
+    acc0 = A::mfma16(A::dq8s(X.z, X.w), xf[1], acc0);
+    acc1 = A::mfma16(A::dq8s(Y.z, Y.w), xf[3], acc1);
     if (s + D < ST) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) wr[s + D][h] = load_stream16(wp[h] + 128 * kst(s + D + rot));
@@ -479,7 +479,7 @@ __global__ __launch_bounds__(64 * gux::kWaves) void gateup_xlds_kernel(
       store16(slot + wdst[1], wt[t][1]);
       const uint4 X = *reinterpret_cast<const uint4 *>(slot + xr_off + (((2 * g) ^ xsw) << 4));
       const uint4 Y = *reinterpret_cast<const uint4 *>(slot + xr_off + (((2 * g + 1) ^ xsw) << 4));
-      const uint4 a0 = A::dq8(X.x, X.y), a1 = A::dq8(X.z, X.w), a2 = A::dq8(Y.x, Y.y), a3 = A::dq8(Y.z, Y.w);
+      const uint4 a0 = A::dq8s(X.x, X.y), a1 = A::dq8s(X.z, X.w), a2 = A::dq8s(Y.x, Y.y), a3 = A::dq8s(Y.z, Y.w);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         acc[t][mt] = A::mfma16(a0, xf[mt][0], acc[t][mt]);

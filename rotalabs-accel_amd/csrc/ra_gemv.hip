@@ -132,10 +132,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(const uint16_t *__restrict__ 
       for (int t = 0; t < NT; ++t) {
         const uint4 c0 = *reinterpret_cast<const uint4 *>(slot + t * 2048 + r_off0);
         const uint4 c1 = *reinterpret_cast<const uint4 *>(slot + t * 2048 + r_off1);
-        acc[t] = A::mfma16(A::dq8(c0.x, c0.y), xf[0], acc[t]);
-        acc[t] = A::mfma16(A::dq8(c0.z, c0.w), xf[1], acc[t]);
-        acc[t] = A::mfma16(A::dq8(c1.x, c1.y), xf[2], acc[t]);
-        acc[t] = A::mfma16(A::dq8(c1.z, c1.w), xf[3], acc[t]);
+        acc[t] = A::mfma16(A::dq8s(c0.x, c0.y), xf[0], acc[t]);
+        acc[t] = A::mfma16(A::dq8s(c0.z, c0.w), xf[1], acc[t]);
+        acc[t] = A::mfma16(A::dq8s(c1.x, c1.y), xf[2], acc[t]);
+        acc[t] = A::mfma16(A::dq8s(c1.z, c1.w), xf[3], acc[t]);
       }
     }
   }

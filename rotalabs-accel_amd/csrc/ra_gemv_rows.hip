@@ -37,7 +37,7 @@ __device__ __forceinline__ float dot16(const uint4 &w, const uint4 &xa, const ui
 
 template <>
 __device__ __forceinline__ float dot16<RA_F16>(const uint4 &w, const uint4 &xa, const uint4 &xb, float sum) {
-  const uint4 lo = dq8_f16(w.x, w.y), hi = dq8_f16(w.z, w.w);
+  const uint4 lo = dq8_f16_cvt(w.x, w.y), hi = dq8_f16_cvt(w.z, w.w);
   sum = __builtin_amdgcn_fdot2(bitcast<f16x2>(lo.x), bitcast<f16x2>(xa.x), sum, false);
   sum = __builtin_amdgcn_fdot2(bitcast<f16x2>(lo.y), bitcast<f16x2>(xa.y), sum, false);
   sum = __builtin_amdgcn_fdot2(bitcast<f16x2>(lo.z), bitcast<f16x2>(xa.z), sum, false);

@@ -91,8 +91,8 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int t = 0; t < NTW; ++t) {
-        const uint4 a0 = A::dq8(wv[u][t].x, wv[u][t].y);
-        const uint4 a1 = A::dq8(wv[u][t].z, wv[u][t].w);
+        const uint4 a0 = A::dq8s(wv[u][t].x, wv[u][t].y);
+        const uint4 a1 = A::dq8s(wv[u][t].z, wv[u][t].w);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           acc[t][mt] = A::mfma16(a0, xa[u][mt], acc[t][mt]);
@@ -121,8 +121,8 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
     }
 #pragma unroll
     for (int t = 0; t < NTW; ++t) {
-      const uint4 a0 = A::dq8(wv[t].x, wv[t].y);
-      const uint4 a1 = A::dq8(wv[t].z, wv[t].w);
+      const uint4 a0 = A::dq8s(wv[t].x, wv[t].y);
+      const uint4 a1 = A::dq8s(wv[t].z, wv[t].w);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         acc[t][mt] = A::mfma16(a0, xa[mt], acc[t][mt]);

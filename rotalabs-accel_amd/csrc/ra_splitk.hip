@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
       for (int t = 0; t < NTW; ++t) {
         const uint2 a8 = *reinterpret_cast<const uint2 *>(ws + (16 * t + r) * 128 +
                                                           (((2 * q + (g >> 1)) ^ wsw) << 4) + 8 * (g & 1));
-        const uint4 a = A::dq8(a8.x, a8.y);
+        const uint4 a = A::dq8s(a8.x, a8.y);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[t][mt] = A::mfma16(a, xf[mt], acc[t][mt]);
       }

@@ -271,7 +271,7 @@ struct DmaTile {
   static constexpr int SMAX = STAGE <= 24 * 1024 ? SMAX_SMALL : 4;
   static constexpr int S = (160 * 1024) / STAGE < SMAX ? (160 * 1024) / STAGE : SMAX;
   static_assert(A_BYTES % 4096 == 0 && B_BYTES % 4096 == 0, "copies must split evenly over 4 waves");
-  static_assert(S >= 2 && S <= 8, "2 to 8 stages");
+  static_assert(S >= 2 && S <= 13, "2 to 13 stages");
   static_assert((S - 1) * COPIES <= 63, "vmcnt is a 6-bit counter");
 };
 
@@ -327,6 +327,14 @@ __global__ __launch_bounds__(256, 1) void tiled_dma_kernel(const uint16_t *__res
   static_assert(!GU || BNB % 2 == 0, "gate/up pairing needs an even number of column blocks");
   constexpr int OUTN = GU ? BN / 2 : BN;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STAGE];
+#ifdef RA_TRACE
+  // Trace builds only: per-workgroup timestamps (constant 100 MHz clock) of
+  // entry, first tile ready, end of the K loop and end of the epilogue's
+  // stores, written to `part` (unused by the non-split kernel).
+  const uint64_t tr_entry = __builtin_amdgcn_s_memrealtime();
+  const uint64_t tr_entry_clk = __builtin_amdgcn_s_memtime();
+  uint64_t tr_ready = 0, tr_kend = 0;
+#endif
 
   // ---- tile coordinates (XCD-aware, grouped along M as in tiled_kernel) ----
   const int T = tiles_m * tiles_n;
@@ -464,9 +472,15 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
     _Pragma("unroll") for (int bj = 0; bj < BNB; ++bj) FB[bj] = *reinterpret_cast<const uint4 *>(   \
         base_ + b_row_off + bj * 32 * 64 + (((2 * (p_) + g) ^ b_sw) << 4));                         \
   }
+// The 64-row tiles (one 32-row block per wave; M <= 64 and the split plans)
+// spend more VALU than MFMA cycles per sub-step on dequantisation and take
+// the 1-VALU-per-value conversion (M=64 K=4096 N=11008: 19.7 -> 18.9 us);
+// the large tiles keep the magic-number form, which their scheduling groups
+// interleave with the MFMAs (the opaque asm form measured 2 % slower there).
+#define RA_DQ_(a_, b_) (BMB == 1 ? Ac::dq8s(a_, b_) : Ac::dq8(a_, b_))
 #define RA_DEQ(h_, FB, BQ)                                                                          \
   _Pragma("unroll") for (int bj = 0; bj < BNB; ++bj) BQ[bj] =                                       \
-      (h_) ? Ac::dq8(FB[bj].z, FB[bj].w) : Ac::dq8(FB[bj].x, FB[bj].y);
+      (h_) ? RA_DQ_(FB[bj].z, FB[bj].w) : RA_DQ_(FB[bj].x, FB[bj].y);
 #define RA_MMA(FA, BQ)                                                                              \
   _Pragma("unroll") for (int bi = 0; bi < BMB; ++bi)                                                \
       _Pragma("unroll") for (int bj = 0; bj < BNB; ++bj) acc[bi][bj] = Ac::mfma32(FA[bi], BQ[bj], acc[bi][bj]);
@@ -533,6 +547,9 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
     if (s < KT) RA_ISSUE(s, s);
   wait_tiles<COPIES, S - 1>(min(KT, S) - 1);
   asm volatile("s_barrier" ::: "memory");
+#ifdef RA_TRACE
+  tr_ready = __builtin_amdgcn_s_memrealtime();
+#endif
   RA_READ_A(0, 0, fa[0]);
   RA_READ_B(0, 0, fbr[0]);
   RA_DEQ(0, fbr[0], bq[0]);
@@ -580,12 +597,16 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
 #undef RA_SUBSTEPS_012
 #undef RA_INTERLEAVE
 #undef RA_DEQ
+#undef RA_DQ_
 #undef RA_MMA
 #undef RA_READ_B
 #undef RA_READ_A
 #undef RA_ISSUE
 #undef RA_ISSUE_PART
 
+#ifdef RA_TRACE
+  tr_kend = __builtin_amdgcn_s_memrealtime();
+#endif
   if constexpr (SPLIT) {
     if (nsplit > 1) {
       // Partial sums through the level all XCDs share (sc1 stores / loads).
@@ -705,6 +726,22 @@ constexpr int P1 = (COPIES + 2) / 3, P2 = (2 * COPIES + 2) / 3;
     if (guard) store_blocks(T_{}, F_{});
     else store_blocks(F_{}, F_{});
   }
+#ifdef RA_TRACE
+  if constexpr (!SPLIT) {
+    if (part != nullptr) {
+      wait_vmcnt<0>();
+      const uint64_t tr_end = __builtin_amdgcn_s_memrealtime();
+      const uint64_t tr_end_clk = __builtin_amdgcn_s_memtime();
+      const uint32_t hwid = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+      const uint32_t xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);
+      if (lane == 0) {
+        uint64_t *rec = reinterpret_cast<uint64_t *>(part) + ((size_t)blockIdx.x * 4 + wid) * 8;
+        rec[0] = tr_entry; rec[1] = tr_ready; rec[2] = tr_kend; rec[3] = tr_end;
+        rec[4] = ((uint64_t)xcc << 32) | hwid; rec[5] = tr_entry_clk; rec[6] = tr_end_clk; rec[7] = (uint64_t)t;
+      }
+    }
+  }
+#endif
 }
 
 static bool tiled_shape_ok(int x_dt, const void *x, int64_t ldx, const int8_t *w, int64_t ldw, int64_t ldy,
@@ -876,6 +913,10 @@ static void launch_dma_split(const GemmArgs &a, const TiledSplitPlan &p, void *w
                      p.nsplit, p.ksplit, part, cnt);
 }
 
+#ifdef RA_TRACE
+extern void *g_trace_buf;
+#endif
+
 template <int DT, bool GU, int BMB, int BNB, int WR, int SM = 4>
 static void launch_dma(const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
                        const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K,
@@ -895,9 +936,14 @@ static void launch_dma(const void *x, int64_t ldx, const int8_t *w, int64_t ldw,
       const void *bi = bias ? static_cast<const void *>(static_cast<const char *>(bias) + ns * bias_sz) : nullptr;
       const int tiles_m = (int)((Mi + G::BM - 1) / G::BM);
       const int tiles_n = (int)((Ni + OUTN - 1) / OUTN);
+#ifdef RA_TRACE
+      float *trace = reinterpret_cast<float *>(g_trace_buf);  // trace builds: per-workgroup timestamps
+#else
+      float *trace = nullptr;
+#endif
       hipLaunchKernelGGL((tiled_dma_kernel<DT, GU, BMB, BNB, WR, SM>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s,
                          xi, ldx, w + ns * ldw, ldw, si, bi, bias_dt, yi, ldy, (int)Mi, (int)Ni, (int)K, tiles_m,
-                         tiles_n, 1, 0, nullptr, nullptr);
+                         tiles_n, 1, 0, trace, nullptr);
     }
   }
 }
@@ -957,12 +1003,25 @@ static void launch_dma_auto(const void *x, int64_t ldx, const int8_t *w, int64_t
   if (forced == 5) c = {8, 2, 1, 0};
   if (forced == 6 && !GU) c = {4, 3, 2, 0};
   if (forced == 7) return launch_dma<DT, GU, 4, 4, 2>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  if constexpr (!GU) {
+    if (forced == 8) return launch_dma<DT, GU, 6, 2, 1>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+    if (forced == 9) return launch_dma<DT, GU, 7, 2, 1>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+  }
 #else
   (void)forced;
 #endif
   // Up to 64 rows: 64 x 64 tiles (2 x 2 waves of one 32 x 32 block each),
   // six K tiles of copies in flight.
   if constexpr (!GU) {
+#ifdef RA_TUNING
+    // Tuning builds only: the small tile with deeper copy pipelines.
+    if (M <= kSmallTileMaxM && forced >= 10 && forced <= 13) {
+      if (forced == 10) return launch_dma<DT, GU, 1, 1, 2, 8>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+      if (forced == 11) return launch_dma<DT, GU, 1, 1, 2, 10>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+      if (forced == 12) return launch_dma<DT, GU, 1, 1, 2, 12>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+      return launch_dma<DT, GU, 1, 1, 2, 4>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
+    }
+#endif
     if (M <= kSmallTileMaxM)
       return launch_dma<DT, GU, 1, 1, 2, 6>(x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, s);
   }
