@@ -68,7 +68,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--only", choices=("all", "decode", "prefill", "prefill_large", "mlp", "w8a8", "shapes",
-                                      "ceiling"),
+                                      "ceiling", "tile-trace"),
                    default="all",
                    help="run one workload only (for profiler runs)")
     p.add_argument("--no-mlp", action="store_true", help="skip the fused-MLP timing")
@@ -533,6 +533,102 @@ PROBE_SRC = os.path.join(HERE, "bench_probe.hip")
 PROBE_LIB = os.path.join(HERE, "bench_probe.so")
 
 
+TRACE_LIB = os.path.join(HERE, "bench_trace.so")
+
+
+def build_trace_lib(force: bool = False) -> str:
+    """Compile the library's sources with -DRA_TUNING -DRA_TRACE (the tiled
+    kernel then writes per-workgroup timestamps to a buffer set with
+    ra_tune_trace) into bench_trace.so beside this script, unless a build
+    newer than every source exists. A measurement build: never loaded by the
+    package unless ROTACCEL_LIB points at it."""
+    import glob
+    import importlib.util
+    import subprocess
+    csrc = os.path.join(HERE, "rotalabs-accel_amd", "csrc")
+    srcs = sorted(glob.glob(os.path.join(csrc, "*.hip")))
+    newest = max(os.path.getmtime(f) for f in srcs + glob.glob(os.path.join(csrc, "*.h")))
+    if not force and os.path.exists(TRACE_LIB) and os.path.getmtime(TRACE_LIB) >= newest:
+        return TRACE_LIB
+    spec = importlib.util.spec_from_file_location(
+        "rotalabs_accel_build", os.path.join(HERE, "rotalabs-accel_amd", "rotalabs_accel", "_build.py"))
+    bld = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bld)
+    import concurrent.futures as cf
+    import tempfile
+    with tempfile.TemporaryDirectory() as td:
+        def one(src):
+            obj = os.path.join(td, os.path.basename(src) + ".o")
+            res = subprocess.run([bld._hipcc(), *bld.compile_flags(), "-DRA_TUNING", "-DRA_TRACE", "-c", src, "-o", obj],
+                                 capture_output=True, text=True)
+            if res.returncode != 0:
+                raise RuntimeError(f"trace build failed for {src}:\n{res.stderr}")
+            return obj
+        with cf.ThreadPoolExecutor(min(8, len(srcs))) as ex:
+            objs = list(ex.map(one, srcs))
+        tmp = TRACE_LIB + ".tmp"
+        res = subprocess.run([bld._hipcc(), f"--offload-arch={bld.ARCH}", "-shared", "-fPIC", *objs, "-o", tmp],
+                             capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"trace link failed:\n{res.stderr}")
+    os.replace(tmp, TRACE_LIB)
+    return TRACE_LIB
+
+
+def run_tile_trace(args, dev):
+    """Per-workgroup timeline of the tiled GEMM (the bench_trace.so build):
+    one traced launch per run after untimed launches on cycled weight copies;
+    each workgroup's entry, first K tile ready (prologue copies landed),
+    end of the K loop and end of the epilogue (its stores complete) on the
+    100 MHz constant clock, plus its shader-clock cycles. Returns a dict."""
+    import ctypes
+    import statistics as st
+    import torch
+    import rotalabs_accel as ra
+    from workloads import gemm_case
+    M, K, N = (int(v) for v in (args.shape or "64,4096,11008").split(","))
+    tl = ctypes.CDLL(os.environ["ROTACCEL_LIB"])
+    tl.ra_tune_trace.argtypes = [ctypes.c_void_p]
+    buf = torch.zeros(1 << 20, dtype=torch.int64, device=dev)
+    c = gemm_case(M, K, N, 6, device=dev, outlier_rows=M > 1)
+    ncop = max(3, -(-600_000_000 // (N * K)))
+    copies = [c.q] + [c.q.clone() for _ in range(ncop - 1)]
+    for i in range(3 * ncop):
+        ra.int8_gemm(c.x, copies[i % ncop], c.s)
+    torch.cuda.synchronize()
+    runs = []
+    for r in range(3):
+        buf.zero_()
+        for i in range(4):
+            ra.int8_gemm(c.x, copies[(r * 5 + i) % ncop], c.s)
+        tl.ra_tune_trace(ctypes.c_void_p(buf.data_ptr()))
+        ra.int8_gemm(c.x, copies[(r * 5 + 4) % ncop], c.s)
+        tl.ra_tune_trace(None)
+        torch.cuda.synchronize()
+        recs = [x for x in buf.view(-1, 8).cpu().tolist() if x[0] != 0]
+        if not recs:
+            raise RuntimeError("no trace records: the shape does not run the traced tiled kernel")
+        t0 = min(x[0] for x in recs)
+        q = lambda a: {"min": round(min(a), 2), "median": round(st.median(a), 2), "max": round(max(a), 2)}
+        rec = {"workgroups": len(recs) // 4, "span_us": round((max(x[3] for x in recs) - t0) / 100.0, 2),
+               "entry_us": q([(x[0] - t0) / 100.0 for x in recs]),
+               "prologue_us": q([(x[1] - x[0]) / 100.0 for x in recs]),
+               "k_loop_us": q([(x[2] - x[1]) / 100.0 for x in recs]),
+               "epilogue_us": q([(x[3] - x[2]) / 100.0 for x in recs]),
+               "shader_clock_ghz": q([(x[6] - x[5]) / max(1, x[3] - x[0]) / 10.0 for x in recs])}
+        # K loop by XCD (hardware XCC id) for the workgroups of the first round (entered within 5 us)
+        # and the later ones
+        for label, first in (("k_loop_us_by_xcd_round1", True), ("k_loop_us_by_xcd_later", False)):
+            by = {}
+            for x in recs:
+                if ((x[0] - t0) / 100.0 < 5.0) == first:
+                    by.setdefault(int(x[4] >> 32), []).append((x[2] - x[1]) / 100.0)
+            rec[label] = {str(k): round(st.median(v), 2) for k, v in sorted(by.items())}
+        log(f"tile trace M={M} K={K} N={N} run {r}: {rec}")
+        runs.append(rec)
+    return {"workload": f"tiled GEMM M={M} K={K} N={N} fp16, per-workgroup timeline (trace build)", "runs": runs}
+
+
 def build_probe(force: bool = False) -> str:
     """Compile the measurement probe (bench_probe.hip, a plain streaming read
     with the decode kernels' access pattern; not part of the library) into
@@ -700,6 +796,8 @@ def main():
               "multi-GPU sharding is design-only.", file=sys.stderr)
         sys.exit(2)
 
+    if args.only == "tile-trace":  # the trace build of the library, loaded in place of the release one
+        os.environ["ROTACCEL_LIB"] = build_trace_lib()
     import torch
     from rotalabs_accel import _backend
     from workloads import gemm_bytes
@@ -715,6 +813,10 @@ def main():
     _backend.load()
     props = torch.cuda.get_device_properties(dev)
     log(f"device {props.name} ({getattr(props, 'gcnArchName', '?')}), {props.multi_processor_count} CUs")
+
+    if args.only == "tile-trace":
+        print(json.dumps(run_tile_trace(args, dev)), flush=True)
+        return
 
     # ---------------- decode M=1 (headline) ----------------
     M, K, N, seed = DECODE
