@@ -28,6 +28,7 @@ int g_batch_xlds = 0;
 int g_batch_xd = 0;
 int g_sk_s = 0;
 int g_sk_dmax = 0;
+int g_sk_x1 = 0;
 int g_tiled_split = 0;
 int g_w8a8_mode = 0;
 int g_rows_lds = 0;
@@ -141,6 +142,7 @@ void ra_tune_batch_nw(int nw) { ra::g_batch_nw = nw; }
 void ra_tune_batch_xlds(int v) { ra::g_batch_xlds = v; }
 void ra_tune_batch_xd(int v) { ra::g_batch_xd = v; }
 void ra_tune_sk(int s, int dmax) { ra::g_sk_s = s; ra::g_sk_dmax = dmax; }
+void ra_tune_sk_x1(int off) { ra::g_sk_x1 = off; }
 void ra_tune_tiled_split(int v) { ra::g_tiled_split = v; }
 void ra_tune_w8a8(int mode) { ra::g_w8a8_mode = mode; }
 void ra_tune_rows_lds(int v) { ra::g_rows_lds = v; }

@@ -109,6 +109,7 @@ __device__ __forceinline__ void static_for_int(F &&f) {
 
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -252,6 +253,13 @@ struct Act<RA_F16> {
   static __device__ __forceinline__ f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(bitcast<f16x8>(a), bitcast<f16x8>(b), c, 0, 0, 0);
   }
+  // c + sum of the 8 products a[i] * b[i] (v_dot2 on element pairs, fp32 sums)
+  static __device__ __forceinline__ float dot8(uint4 a, uint4 b, float c) {
+    c = __builtin_amdgcn_fdot2(bitcast<f16x2>(a.x), bitcast<f16x2>(b.x), c, false);
+    c = __builtin_amdgcn_fdot2(bitcast<f16x2>(a.y), bitcast<f16x2>(b.y), c, false);
+    c = __builtin_amdgcn_fdot2(bitcast<f16x2>(a.z), bitcast<f16x2>(b.z), c, false);
+    return __builtin_amdgcn_fdot2(bitcast<f16x2>(a.w), bitcast<f16x2>(b.w), c, false);
+  }
   static __device__ __forceinline__ uint16_t out(float v) { return f32_to_f16(v); }
   static __device__ __forceinline__ float in(uint16_t b) { return f16_to_f32(b); }
   static __device__ __forceinline__ float rnd(float v) { return (float)(_Float16)v; }
@@ -266,6 +274,12 @@ struct Act<RA_BF16> {
   }
   static __device__ __forceinline__ f32x16 mfma32(uint4 a, uint4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(bitcast<bf16x8>(a), bitcast<bf16x8>(b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float dot8(uint4 a, uint4 b, float c) {
+    c = __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(a.x), bitcast<bf16x2>(b.x), c, false);
+    c = __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(a.y), bitcast<bf16x2>(b.y), c, false);
+    c = __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(a.z), bitcast<bf16x2>(b.z), c, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(a.w), bitcast<bf16x2>(b.w), c, false);
   }
   static __device__ __forceinline__ uint16_t out(float v) { return f32_to_bf16(v); }
   static __device__ __forceinline__ float in(uint16_t b) { return bf16_to_f32(b); }

@@ -41,7 +41,7 @@
 
 namespace ra {
 #ifdef RA_TUNING
-extern int g_sk_s, g_sk_dmax;  // tuning builds: forced split count, pipeline depth cap
+extern int g_sk_s, g_sk_dmax, g_sk_x1;  // tuning builds: forced split count, depth cap, extra-row form
 #endif
 
 namespace sk {
@@ -62,16 +62,22 @@ constexpr int kMaxCounters = (int)(kCounterBytes / sizeof(int));
 constexpr int ntw(int tw, bool gu) { return gu ? 2 * tw : tw; }
 constexpr int x_slot(int mt) { return mt * 4096; }            // [16*MT rows][256 bytes]
 constexpr int w_slot(int tw, bool gu) { return ntw(tw, gu) * 2048; }  // per wave: [16*NTW rows][128 bytes]
-constexpr int lds_bytes(int mt, int tw, bool gu, int d) { return (d + 1) * x_slot(mt) + d * NW * w_slot(tw, gu); }
-constexpr int copies(int mt, int tw, bool gu) { return 2 * ntw(tw, gu) + mt; }  // per wave per stage
+constexpr int x1_slot = 256;                                  // the extra row: [128 k] of 2 bytes
+constexpr int lds_bytes(int mt, int tw, bool gu, int d, int x1 = 0) {
+  return (d + 1) * (x_slot(mt) + x1 * x1_slot) + d * NW * w_slot(tw, gu);
+}
+constexpr int copies(int mt, int tw, bool gu, int x1 = 0) { return 2 * ntw(tw, gu) + mt + x1; }  // per wave per stage
 // Deepest pipeline that fits LDS and the 6-bit vmcnt.
-constexpr int depth(int mt, int tw, bool gu, int dmax = kMaxD) {
+constexpr int depth(int mt, int tw, bool gu, int dmax = kMaxD, int x1 = 0) {
   int d = dmax;
-  while (d > 2 && (lds_bytes(mt, tw, gu, d) > kLds || (d - 1) * copies(mt, tw, gu) > 63)) --d;
+  while (d > 2 && (lds_bytes(mt, tw, gu, d, x1) > kLds || (d - 1) * copies(mt, tw, gu, x1) > 63)) --d;
   return d;
 }
-// fp32 values of one unit's partial sums: per wave NTW x MT fragments of 64 lanes x 4.
-constexpr int part_floats(int mt, int tw, bool gu) { return NW * ntw(tw, gu) * mt * 256; }
+// fp32 partial sums of one wave per split: NTW x MT fragments of 64 lanes x 4,
+// then (extra row) the NTW row sums per lane, packed 4 to a 16-byte group.
+constexpr int x1_groups(int tw, bool gu) { return (ntw(tw, gu) + 3) / 4; }
+constexpr int wave_floats(int mt, int tw, bool gu, int x1) { return (ntw(tw, gu) * mt + x1 * x1_groups(tw, gu)) * 256; }
+constexpr int part_floats(int mt, int tw, bool gu, int x1 = 0) { return NW * wave_floats(mt, tw, gu, x1); }
 }  // namespace sk
 
 // Non-temporal direct-to-LDS copy (the weight rows are read once per call).
@@ -93,7 +99,11 @@ __device__ __forceinline__ void wait_stages(int younger) {
   wait_vmcnt<0>();
 }
 
-template <int DT, int MT, int TW, bool GU, int DMAX = sk::kMaxD>
+// X1 = 1: M = 16*MT + 1. The MFMA tiles cover rows 0 .. 16*MT-1 and the last
+// row is a dot product on the VALU (v_dot2 over the weights the MFMA tiles
+// already dequantised), instead of a second, almost empty 16-row MFMA tile
+// (whose activation copies, LDS reads and MFMAs cost as much as a full one).
+template <int DT, int MT, int TW, bool GU, int X1, int DMAX = sk::kMaxD>
 __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__ xb, int64_t ldx,
                                                         const char *__restrict__ wb, int64_t ldw,
                                                         const float *__restrict__ scale,
@@ -104,13 +114,14 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
   using A = Act<DT>;
   using namespace sk;
   constexpr int NTW = ntw(TW, GU);
-  constexpr int WL = 2 * NTW;  // weight copies per stage per wave
-  constexpr int CP = WL + MT;  // copies per stage per wave
-  constexpr int D = depth(MT, TW, GU, DMAX);
+  constexpr int WL = 2 * NTW;       // weight copies per stage per wave
+  constexpr int CP = WL + MT + X1;  // copies per stage per wave
+  constexpr int D = depth(MT, TW, GU, DMAX, X1);
   constexpr int XS = x_slot(MT), WS = w_slot(TW, GU);
-  constexpr int XRING = 0, WRING = (D + 1) * XS;
+  constexpr int XRING = 0, WRING = (D + 1) * XS, X1RING = WRING + D * NW * WS;
   constexpr int R = NW * TW * 16;  // output columns per unit
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes(MT, TW, GU, D)];
+  static_assert(X1 == 0 || X1 == 1, "at most one row past the MFMA tiles");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes(MT, TW, GU, D, X1)];
   __shared__ int s_last;
 
   // Unit -> (row block, split). Units of one row block are dealt to one XCD
@@ -175,6 +186,10 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
   const uint32_t lds0 = lds_offset(lds);
   const uint32_t wdst = lds0 + WRING + (uint32_t)wid * WS;
   const uint32_t xdst = lds0 + XRING + (uint32_t)(wid * MT) * 1024;
+  // Extra row (X1): the stage's 256 bytes of row 16*MT, 64 per wave, copied
+  // by lanes 0..3 (16 bytes each, k = 32*wid + 8*lane .. +7).
+  const uint32_t x1voff = (uint32_t)(((int64_t)(16 * MT) * ldx) * 2 + 64 * wid + 16 * (lane & 3));
+  const uint32_t x1dst = lds0 + X1RING + (uint32_t)(64 * wid);
 
   auto issue = [&](int st) __attribute__((always_inline)) {
     const int sr = st + rot < nst ? st + rot : st + rot - nst;
@@ -187,6 +202,9 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
     for (int j = 0; j < WL; ++j) dma16s_nt(sw, wvoff[j], wd + 1024u * j);
 #pragma unroll
     for (int c = 0; c < MT; ++c) dma16s<0, true>(sx, xvoff[c], xd + 1024u * c);
+    if constexpr (X1 != 0) {
+      if (lane < 4) dma16s<0, true>(sx, x1voff, x1dst + (uint32_t)((st % (D + 1)) * x1_slot));
+    }
   };
 
   f32x4 acc[NTW][MT];
@@ -194,6 +212,11 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
   for (int t = 0; t < NTW; ++t)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Extra row: lane (r, g) sums weight row 16t + r against row 16*MT over
+  // its k = 8g .. 8g+7 of every 32; the four g are added after the loop.
+  float acc1[NTW];
+#pragma unroll
+  for (int t = 0; t < NTW; ++t) acc1[t] = 0.f;
 
   for (int p = 0; p < D; ++p)
     if (p < nst) issue(p);
@@ -204,12 +227,15 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
     __syncthreads();  // every wave's copies of stage st have landed
     const uint8_t *ws = lds + WRING + ((st % D) * NW + wid) * WS;
     const uint8_t *xs = lds + XRING + (st % (D + 1)) * XS;
+    const uint8_t *x1s = lds + X1RING + (st % (D + 1)) * x1_slot;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       uint4 xf[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
         xf[mt] = *reinterpret_cast<const uint4 *>(xs + (16 * mt + r) * 256 + (((4 * q + g) ^ r) << 4));
+      uint4 x1f;
+      if constexpr (X1 != 0) x1f = *reinterpret_cast<const uint4 *>(x1s + 64 * q + 16 * g);  // 16-lane broadcast
 #pragma unroll
       for (int t = 0; t < NTW; ++t) {
         const uint2 a8 = *reinterpret_cast<const uint2 *>(ws + (16 * t + r) * 128 +
@@ -217,6 +243,7 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
         const uint4 a = A::dq8s(a8.x, a8.y);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[t][mt] = A::mfma16(a, xf[mt], acc[t][mt]);
+        if constexpr (X1 != 0) acc1[t] = A::dot8(a, x1f, acc1[t]);
       }
     }
     if (st + D < nst) {
@@ -228,13 +255,23 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
     }
   }
 
+  if constexpr (X1 != 0) {
+    // the four k groups g (lanes r, r+16, r+32, r+48); every lane gets the row sum
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) {
+      acc1[t] += __shfl_xor(acc1[t], 16, 64);
+      acc1[t] += __shfl_xor(acc1[t], 32, 64);
+    }
+  }
+
   if (S > 1) {
     // The partial sums are exchanged with device-scope stores and loads
     // (sc1), which write through to / read from the level shared by all
     // XCDs; a release / acquire fence would instead write back and
     // invalidate the whole L2 of the XCD, a cost every unit would pay.
-    constexpr int FR = NTW * MT * 256;  // floats per wave and split
-    // this row block's partial sums: [S][NW][NTW * MT fragments][64 lanes][4]
+    constexpr int FR = wave_floats(MT, TW, GU, X1);  // floats per wave and split
+    constexpr int G1 = x1_groups(TW, GU);
+    // this row block's partial sums: [S][NW][NTW * MT fragments + G1 groups][64 lanes][4]
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         part + (size_t)rb * S * NW * FR, 0, (int)(S * NW * FR * sizeof(float)), kRsrcWord3);
     const uint32_t lo = (uint32_t)(wid * FR + lane * 4) * 4u;  // byte offset of this lane in split 0
@@ -243,6 +280,15 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
         store_dev16(rs, lo + (uint32_t)(s * NW * FR + (t * MT + mt) * 256) * 4u, acc[t][mt]);
+    if constexpr (X1 != 0) {
+#pragma unroll
+      for (int q1 = 0; q1 < G1; ++q1) {
+        f32x4 e;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e[i] = 4 * q1 + i < NTW ? acc1[4 * q1 + i] : 0.f;
+        store_dev16(rs, lo + (uint32_t)(s * NW * FR + (NTW * MT + q1) * 256) * 4u, e);
+      }
+    }
     wait_vmcnt<0>();  // this wave's partial sums are stored
     __syncthreads();  // and every wave's
     if (threadIdx.x == 0)
@@ -285,6 +331,26 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
     for (int t = 0; t < NTW; ++t)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[t][mt] = sum[t][mt];
+    if constexpr (X1 != 0) {
+      // the extra row's sums, in split order 0..S-1 as above (one round trip per split)
+#pragma unroll
+      for (int q1 = 0; q1 < G1; ++q1) {
+        f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s2 = 0; s2 < S; ++s2) {
+          f32x4 cur;
+          if (s2 == s) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cur[i] = 4 * q1 + i < NTW ? acc1[4 * q1 + i] : 0.f;
+          } else {
+            cur = load_dev16(rs, lo + (uint32_t)(s2 * NW * FR + (NTW * MT + q1) * 256) * 4u);
+          }
+          tot = s2 == 0 ? cur : tot + cur;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (4 * q1 + i < NTW) acc1[4 * q1 + i] = tot[i];
+      }
+    }
     if (threadIdx.x == 0) __hip_atomic_store(&cnt[rb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
@@ -306,6 +372,17 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
           yrow[n] = swiglu_out<A>(acc[t][mt][e] * scale[n], acc[TW + t][mt][e] * scale[N + n]);
         else
           yrow[n] = A::out(epilogue_value(acc[t][mt][e], scale, bias, bias_dt, n));
+      }
+    }
+    if constexpr (X1 != 0) {
+      // row 16*MT, column 16*(wid*TW + t) + r, stored by the lanes of group g == t % 4
+      const int n = n0 + 16 * (wid * TW + t % TW) + r;
+      if (g == (t & 3) && n < N) {
+        uint16_t *yrow = y + (int64_t)(16 * MT) * ldy;
+        if (GU)
+          yrow[n] = swiglu_out<A>(acc1[t] * scale[n], acc1[TW + t] * scale[N + n]);
+        else
+          yrow[n] = A::out(epilogue_value(acc1[t], scale, bias, bias_dt, n));
       }
     }
   }
@@ -330,6 +407,14 @@ bool sk_shape_ok(int x_dt, const void *x, int64_t ldx, const int8_t *w, int64_t 
   return true;
 }
 
+bool x1_allowed() {
+#ifdef RA_TUNING
+  return g_sk_x1 == 0;  // tuning builds: 1 turns the extra-row form off
+#else
+  return true;
+#endif
+}
+
 int device_cus() {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
@@ -348,7 +433,15 @@ SplitkPlan splitk_plan(int64_t M, int64_t N, int64_t K, bool gu, bool allow_spli
   SplitkPlan best{};
   best.ok = false;
   if (M < 1 || M > sk::kMaxM || K < sk::KS || K % sk::KS != 0 || N < 1) return best;
-  const int mt = sk_mt(M);
+  int mt = sk_mt(M), x1 = 0;
+  // M = 17 or 33 at K >= 16384: one 16-row MFMA tile fewer, the last row on
+  // the VALU (same-run A/B, us, padded tile -> extra row: M=17 K=28672
+  // N=8192 bf16 49.5 -> 45.6, M=33 K=16384 N=4096 25.3 -> 23.8, M=17 K=16384
+  // N=16384 level; at M=17 K=11008 N=4096 16.3 -> 17.0, so not below 16384)
+  if ((M == 17 || M == 33) && K >= 16384 && x1_allowed()) {
+    mt = (int)(M / 16);
+    x1 = 1;
+  }
   const int cus = device_cus();
   const int64_t stages = K / sk::KS;
   double best_t = 0;
@@ -371,25 +464,25 @@ SplitkPlan splitk_plan(int64_t M, int64_t N, int64_t K, bool gu, bool allow_spli
       const int64_t slots = ((nb + 7) / 8) * 8 * S;  // grid (XCD-grouped row blocks)
       const int64_t rounds = (units + cus - 1) / cus;
       const double wbytes = (double)(ntw * 16 * sk::NW) * kc;
-      const double xbytes = (double)std::min<int64_t>(M, 16 * mt) * kc * 2;
-      const double pbytes = S > 1 ? (double)sk::part_floats(mt, tw, gu) * 4 * (1.0 + 1.0) : 0.0;
+      const double xbytes = (double)std::min<int64_t>(M, 16 * mt + x1) * kc * 2;
+      const double pbytes = S > 1 ? (double)sk::part_floats(mt, tw, gu, x1) * 4 * (1.0 + 1.0) : 0.0;
       const double t = (double)rounds * (wbytes + xbytes + pbytes) + 1e-3 * (double)slots;
       if (!best.ok || t < best_t) {
-        best = SplitkPlan{true, mt, tw, S, (int)kc, (int)nb, false, 0, 0};
+        best = SplitkPlan{true, mt, tw, S, (int)kc, (int)nb, false, 0, 0, x1};
         best_t = t;
       }
     }
   }
   if (best.ok && best.S > 1) {
     best.cnt_bytes = sk::kCounterBytes;
-    best.ws_bytes = best.cnt_bytes + (size_t)best.S * best.nb * sk::part_floats(best.mt, best.tw, gu) * 4;
+    best.ws_bytes = best.cnt_bytes + (size_t)best.S * best.nb * sk::part_floats(best.mt, best.tw, gu, best.x1) * 4;
   }
   return best;
 }
 
 namespace {
 
-template <int DT, int MT, int TW, bool GU>
+template <int DT, int MT, int TW, bool GU, int X1>
 void splitk_go(const SplitkPlan &p, const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
                const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K, void *ws,
                hipStream_t s) {
@@ -398,14 +491,14 @@ void splitk_go(const SplitkPlan &p, const void *x, int64_t ldx, const int8_t *w,
   float *part = ws ? reinterpret_cast<float *>(static_cast<char *>(ws) + p.cnt_bytes) : nullptr;
 #ifdef RA_TUNING
   if (g_sk_dmax == 2 || g_sk_dmax == 3) {  // forced pipeline depth cap
-    auto k = g_sk_dmax == 2 ? splitk_kernel<DT, MT, TW, GU, 2> : splitk_kernel<DT, MT, TW, GU, 3>;
+    auto k = g_sk_dmax == 2 ? splitk_kernel<DT, MT, TW, GU, X1, 2> : splitk_kernel<DT, MT, TW, GU, X1, 3>;
     hipLaunchKernelGGL(k, dim3(grid), dim3(256), 0, s, static_cast<const char *>(x), ldx,
                        reinterpret_cast<const char *>(w), ldw, scale, bias, bias_dt, static_cast<uint16_t *>(y), ldy,
                        (int)M, (int)N, (int)K, p.kc, p.S, p.nb, p.spread ? 1 : 0, part, cnt);
     return;
   }
 #endif
-  hipLaunchKernelGGL((splitk_kernel<DT, MT, TW, GU>), dim3(grid), dim3(256), 0, s,
+  hipLaunchKernelGGL((splitk_kernel<DT, MT, TW, GU, X1>), dim3(grid), dim3(256), 0, s,
                      static_cast<const char *>(x), ldx, reinterpret_cast<const char *>(w), ldw, scale, bias,
                      bias_dt, static_cast<uint16_t *>(y), ldy, (int)M, (int)N, (int)K, p.kc, p.S, p.nb, p.spread ? 1 : 0,
                      part, cnt);
@@ -415,12 +508,14 @@ template <int DT, bool GU>
 void splitk_dispatch(const SplitkPlan &p, const void *x, int64_t ldx, const int8_t *w, int64_t ldw,
                      const float *scale, const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N,
                      int64_t K, void *ws, hipStream_t s) {
-#define RA_SK(MT_, TW_)                                                                                          \
-  if (p.mt == MT_ && p.tw == TW_)                                                                              \
-    return splitk_go<DT, MT_, TW_, GU>(p, x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, ws, s);
-  RA_SK(1, 1) RA_SK(1, 2) RA_SK(1, 3)
-  RA_SK(2, 1) RA_SK(2, 2) RA_SK(2, 3)
-  RA_SK(4, 1) RA_SK(4, 2) RA_SK(4, 3)
+#define RA_SK(MT_, TW_, X1_)                                                                                     \
+  if (p.mt == MT_ && p.tw == TW_ && p.x1 == X1_)                                                               \
+    return splitk_go<DT, MT_, TW_, GU, X1_>(p, x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, ws, s);
+  RA_SK(1, 1, 0) RA_SK(1, 2, 0) RA_SK(1, 3, 0)
+  RA_SK(2, 1, 0) RA_SK(2, 2, 0) RA_SK(2, 3, 0)
+  RA_SK(4, 1, 0) RA_SK(4, 2, 0) RA_SK(4, 3, 0)
+  RA_SK(1, 1, 1) RA_SK(1, 2, 1) RA_SK(1, 3, 1)
+  RA_SK(2, 1, 1) RA_SK(2, 2, 1) RA_SK(2, 3, 1)
 #undef RA_SK
 }
 

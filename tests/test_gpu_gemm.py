@@ -317,10 +317,12 @@ def test_tiled_tile_geometries(gpu, M, K, N, dt):
 
 # Split-K small-batch shapes: many splits (long K, few rows), N tails, one
 # stage per split, every activation-tile count (M <= 16, 32, 64), two rows,
-# and the small-batch (K=4096 N=11008) and MLP down-projection shapes.
+# the small-batch (K=4096 N=11008) and MLP down-projection shapes, and
+# M = 17 / 33 at K >= 16384 (the last row summed on the VALU beside the
+# MFMA tiles).
 SPLITK_SHAPES = [(3, 4096, 11008), (16, 4096, 11008), (64, 4096, 11008), (8, 8192, 256), (17, 8192, 300),
                  (33, 1024, 1000), (64, 128, 64), (5, 28672, 8192), (20, 2048, 77), (40, 512, 3000),
-                 (2, 16384, 700)]
+                 (2, 16384, 700), (17, 16384, 1000), (33, 16384, 520), (17, 28672, 300)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
