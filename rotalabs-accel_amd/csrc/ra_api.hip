@@ -61,6 +61,35 @@ constexpr int64_t kSkinnyMaxM = 64;
 // 15.6-30.2), and at K=8192 N=57344 (88.6 vs 115.6).
 constexpr int64_t kSplitkMinK = 16384;
 
+// M = 1 at K <= 2048 over at least 4096 weight rows: the row GEMV's short
+// rows keep too few bytes in flight per wave, and the small-batch kernel
+// (at K = 2048 its activation-resident form) is ahead, or the skinny
+// split-K kernel at K <= 1536 over 16384+ rows. Same run, bf16, us, row
+// GEMV -> pick: K=2048 N=16384 9.61 -> 7.48, N=11008 7.80 -> 6.45, N=4096
+// 4.45 -> 4.21; K=1024 N=8192 5.57 -> 4.44, N=16384 8.41 -> 6.60 (skinny);
+// K=512 N=4096 4.21 -> 3.25. N=2048 and K >= 3072 stay with the row GEMV
+// (K=3072 N=16384 10.59 against 11.15 for the small-batch kernel).
+int one_row_short_k(const GemmArgs &a) {
+  if (a.M != 1 || a.K > 2048 || a.N < 4096) return 0;
+  if (a.K <= 1536 && a.N >= 16384 && skinny_supported(a)) return RA_VARIANT_SKINNY;
+  return batch_supported(a) ? RA_VARIANT_BATCH : 0;
+}
+
+// M = 33..56 at short K over at most ~12K weight rows: the small-batch
+// kernel is ahead of the 64-row tiles. Same run, bf16, us, tile -> small
+// batch: M=33 K=2048 N=8192 12.24 -> 9.76, K=3072 N=12288 16.58 -> 16.03;
+// M=40 K=1024 N=8192 9.40 -> 7.19, K=2048 N=12288 12.92 -> 12.84; M=48
+// K=1024 N=11008 9.63 -> 9.38, K=2048 N=8192 12.51 -> 11.12; M=56 K=2048
+// N=8192 12.54 -> 11.74. The tiles stay ahead at M=48 K=2048 N=9216 (12.85
+// against 13.07), M=48 K=3072, M=56 K=1024 N=9216, M=64, K >= 4096 (M=33
+// K=4096 N=11008 18.1 against 19.6) and N >= 13824 (M=33 K=2048 12.98
+// against 17.89).
+bool short_k_batch(const GemmArgs &a) {
+  if (a.M < 33 || a.M > 56 || !batch_supported(a)) return false;
+  return (a.M <= 40 && a.K <= 3072 && a.N <= 12288) || (a.K <= 2048 && a.N <= 8192) ||
+         (a.M <= 48 && a.K <= 1024 && a.N <= 12288);
+}
+
 int select_variant(const GemmArgs &a, bool have_ws) {
   if (a.K == 0) return RA_VARIANT_GENERIC;
   // M = 2 runs the small-batch kernels where they apply: the row GEMV
@@ -69,11 +98,14 @@ int select_variant(const GemmArgs &a, bool have_ws) {
   // N=8192 40.3 split K / 38.9 small batch vs 50.0, K=16384 N=16384 44.4 /
   // 47.4 vs 56.2, K=8192 N=57344 81.1 small batch vs 95.0). M = 1 stays with
   // the row GEMV (8.5 vs 9.8 at K=4096 N=11008, 37.3 vs 39.0 at K=28672).
-  if (gemv_rows_supported(a) && (a.M == 1 || !batch_supported(a))) return RA_VARIANT_ROWS;
+  if (gemv_rows_supported(a) && (a.M == 1 || !batch_supported(a))) {
+    const int v = one_row_short_k(a);
+    return v ? v : RA_VARIANT_ROWS;
+  }
   // M = 33..64 with at least 8192 weight rows: the 64-row tiles (K split
   // over workgroups where that pays), also at long K (M=64 K=28672 N=8192:
   // 58.0 us against 65.9 for the split-K kernel).
-  if (tiled_small_selected(a)) return RA_VARIANT_TILED;
+  if (tiled_small_selected(a) && !short_k_batch(a)) return RA_VARIANT_TILED;
   // Split K: long K, or from 16 rows K >= 11008 over at most 4096 weight
   // rows (M=64 K=14336 N=4096: 29.1 us against 55.0 for the small-batch
   // kernel, M=16 K=11008 N=4096 15.0 against 16.3).
@@ -83,6 +115,17 @@ int select_variant(const GemmArgs &a, bool have_ws) {
       (a.K >= kSplitkMinK || (a.M >= 16 && a.K >= 11008 && a.N <= 4096)) &&
       splitk_plan(a.M, a.N, a.K, false, true).S > 1)
     return RA_VARIANT_SPLITK;
+  // The split-K kernel without a split (S = 1, no workspace, with or
+  // without one given) at M = 17..32, K = 2048..4096 over 28672+ weight
+  // rows, where the small-batch kernel needs a second round of workgroups
+  // (same run, bf16, us: M=32 K=4096 N=28672 37.9 -> 29.8, M=24 K=3072
+  // N=40960 36.3 -> 31.4, M=20 K=2048 N=28672 18.3 -> 17.5, M=17 K=4096
+  // N=28672 29.8 -> 28.7; at N=24576 and at K=5120 N=27648 the small-batch
+  // kernel stays ahead).
+  if (a.M >= 17 && a.M <= 32 && a.K >= 2048 && a.K <= 4096 && a.N >= 28672 && splitk_supported(a)) {
+    const SplitkPlan p = splitk_plan(a.M, a.N, a.K, false, true);
+    if (p.ok && p.S == 1) return RA_VARIANT_SPLITK;
+  }
   // M = 3..64: the small-batch kernel (line-wide weight loads, activations
   // read once per 48 rows) where K % 128 == 0, else the split-K MFMA kernel;
   // both measured faster than the LDS GEMV, which stays as a fallback.

@@ -95,6 +95,23 @@ def test_variant_selection_fallbacks():
     assert lib.ra_w8a16_gemm_select(4, 64, 0, 0) == 3      # K == 0 -> generic (bias / zeros)
 
 
+@pytest.mark.parametrize("M,N,K,expect", [
+    # M = 1, K <= 2048 over 4096+ rows: the small-batch kernel (skinny at K <= 1536 over 16384+ rows)
+    (1, 16384, 2048, 6), (1, 4096, 512, 6), (1, 16384, 1024, 1), (1, 2048, 1024, 5), (1, 16384, 3072, 5),
+    (1, 11008, 4096, 5),
+    # M = 33..56 at short K over at most ~12K rows: the small-batch kernel instead of the 64-row tiles
+    (33, 8192, 2048, 6), (40, 12288, 3072, 6), (48, 11008, 1024, 6), (56, 8192, 2048, 6),
+    (48, 9216, 2048, 2), (33, 13824, 2048, 2), (64, 8192, 2048, 2), (33, 11008, 4096, 2),
+    # M = 17..32, K = 2048..4096 over 28672+ rows: the split-K kernel without a split (no workspace)
+    (32, 28672, 4096, 7), (17, 28672, 4096, 7), (20, 40960, 2048, 7), (24, 24576, 4096, 6),
+    (32, 27648, 5120, 6), (16, 28672, 4096, 6)])
+def test_variant_selection_short_k_and_wide(M, N, K, expect):
+    lib = _backend.load()
+    assert lib.ra_w8a16_gemm_select(M, N, K, 1) == expect
+    if expect == 7 and K <= 4096:   # the unsplit split-K kernel needs no workspace
+        assert lib.ra_w8a16_gemm_workspace_size(M, N, K, 1) == 0
+
+
 def test_workspace_of_the_tiled_split_plan():
     """M = 33..64 shapes whose tiled plan splits K (64 x 128 tiles over 4
     workgroups at M=64 K=11008 N=8192) ask for a workspace; the 64 x 64 tile

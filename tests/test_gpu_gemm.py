@@ -349,6 +349,40 @@ def test_splitk_exact_and_repeated(gpu, M, K, N, dt):
             _oracle_check(y1.cpu(), c.x, c.q, c.s)
 
 
+# Shapes where the automatic pick is not the default kernel of the M range:
+# M = 1 at short K (small-batch / skinny kernels instead of the row GEMV),
+# M = 33..56 at short K (small-batch kernel instead of the 64-row tiles), and
+# M = 17..32 at K <= 4096 over 28672+ rows (the split-K kernel without a
+# split). N tails included.
+SELECTION_RULE_SHAPES = [(1, 2048, 16384), (1, 1024, 16390), (1, 512, 4100), (33, 2048, 8192), (40, 3072, 12000),
+                         (48, 1024, 11008), (56, 2048, 8190), (24, 2048, 28672), (32, 4096, 28700), (17, 4096, 28672)]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K,N", SELECTION_RULE_SHAPES)
+def test_selection_rule_shapes_exact_and_oracle(gpu, M, K, N, dt):
+    """The automatic pick at these shapes: exact known answers (with a
+    workspace and without one: the same kernel, bitwise the same output),
+    then a random case against the oracle bound."""
+    lib = _backend.load()
+    sel = lib.ra_w8a16_gemm_select(M, N, K, _backend.dtype_code(dt))
+    print(f"  rule shape M={M} K={K} N={N} {dt}: variant {sel}", flush=True)
+    assert sel != _backend.VARIANT_ROWS or M == 1
+    x, q, s, b, exact = _exact_case(M, K, N, dt, seed=M + K + N, dev=gpu, bias=(N % 2 == 0))
+    y = _run(x, q, s, b, 0).cpu()
+    assert torch.equal(y, exact.to(dt)), f"max err {(y.double() - exact).abs().max()}"
+    c = gemm_case(M, K, N, seed=M + 3, dtype=dt, outlier_rows=M > 1)
+    xg, qg, sg = c.x.to(gpu), c.q.to(gpu), c.s.to(gpu)
+    y1 = ra.int8_gemm(xg, qg, sg)
+    out = torch.empty_like(y1)
+    code = lib.ra_w8a16_gemm(xg.data_ptr(), K, _backend.dtype_code(dt), qg.data_ptr(), K, sg.data_ptr(), None,
+                             _backend.F32, out.data_ptr(), N, M, N, K, _backend.stream_handle(gpu))
+    torch.cuda.synchronize()
+    assert code == 0
+    assert torch.equal(y1, out), "with and without a workspace"
+    _oracle_check(y1.cpu(), c.x, c.q, c.s)
+
+
 def test_splitk_plans_share_one_workspace(gpu):
     """Calls with different split plans (58 row blocks x 4 splits, then 94 x
     2, then 4 x 16) on one stream share its workspace: the counters sit in a
