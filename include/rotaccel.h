@@ -126,10 +126,11 @@ size_t ra_w8a16_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int x_dtype
  * and frees nothing -- for callers that cannot allocate: code under HIP
  * graph capture, serving loops and harnesses that forbid allocation. No
  * counterpart in the reference. Same kernels and results as
- * ra_w8a16_gemm_ws with a workspace; RA_ERR_WORKSPACE when the split-K
- * kernel needs more than 16 MiB (a tiled split plan that needs more runs
- * its tile over all of K instead, as ra_w8a16_gemm_ws does with too small a
- * workspace). Every call on a GPU shares that GPU's array: calls that may
+ * ra_w8a16_gemm_ws with a workspace (split-K plans never need more than
+ * 16 MiB; a tiled split plan that needs more runs its tile over all of K
+ * instead, as ra_w8a16_gemm_ws does with too small a workspace;
+ * RA_ERR_WORKSPACE if a plan ever needed more than the array holds).
+ * Every call on a GPU shares that GPU's array: calls that may
  * overlap on one GPU (several streams) race.
  */
 int ra_w8a16_gemm_noalloc(const void *x, int64_t ldx, int x_dtype,

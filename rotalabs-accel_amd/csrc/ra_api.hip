@@ -29,6 +29,7 @@ int g_batch_xd = 0;
 int g_sk_s = 0;
 int g_sk_dmax = 0;
 int g_sk_x1 = 0;
+int g_sk_tw = 0;
 int g_tiled_split = 0;
 int g_w8a8_mode = 0;
 int g_rows_lds = 0;
@@ -90,6 +91,46 @@ bool short_k_batch(const GemmArgs &a) {
          (a.M <= 48 && a.K <= 1024 && a.N <= 12288);
 }
 
+// Where the split-K kernel is measured ahead (same run, bf16, us, graph
+// replay of cold weights; the other kernel -> split K):
+//  * M = 2..32: K >= 16384 (M=16 K=28672 N=28672 197.0 -> 148.7, M=32
+//    N=14336 131.0 -> 83.1, M=8 K=16384 N=28672 90.4 -> 81.1; M = 2..4 level
+//    within 4 %); from K = 5120 over 14336+ weight rows (M=16 K=5120
+//    N=28672 43.4 -> 29.6, M=2 K=11008 N=28672 62.0 -> 55.4; at N = 57344
+//    with K = 8192 / 14336 and M <= 8 the small-batch kernel stays 2-4 %
+//    ahead); M >= 16 from K = 11008 (M=16 K=11008 N=8192 22.2 -> 20.0);
+//    M >= 24 over at most 4096 rows (M=24 K=8192 N=4096 16.4 -> 14.5);
+//    M = 32 (K=5120 N=8192 16.4 -> 16.0, K=8192 N=8192 22.1 -> 21.2). The
+//    small-batch kernel stays ahead below those (M=8 K=8192 N=8192 15.3
+//    against 16.8, M=24 K=8192 N=8192 18.9 against 21.9).
+//  * M = 33..64 against the 64-row tiles: K >= 14336 (M=33 K=16384 N=16384
+//    74.7 -> 58.4, M=64 K=16384 N=32768 146.7 -> 128.0) except M > 56 over
+//    8192..16384 rows (M=64 K=28672 N=8192 60.5 against 66.2); up to M = 56
+//    K >= 8192 over 32768+ rows (M=33 K=8192 N=32768 73.5 -> 67.5; at M=64
+//    N=57344 the tiles stay ahead, 122.4 against 133.8); at most 4096 rows from
+//    K = 4096, against the small-batch kernel (M=64 K=8192 N=4096 32.8 ->
+//    20.2, M=64 K=4096 N=4096 18.4 -> 14.9).
+bool splitk_wanted(const GemmArgs &a) {
+  if (a.M < 2 || a.M > kSkinnyMaxM) return false;
+  if (a.M <= 32) {
+    if (a.K >= kSplitkMinK) return true;
+    if (a.K < 5120) return false;
+    return a.N >= 14336 || (a.M >= 16 && a.K >= 11008) || (a.M >= 24 && a.N <= 4096) || a.M >= 32;
+  }
+  if (a.N <= 4096) return a.K >= 4096;
+  if (a.K >= 14336) return !(a.M > 56 && a.N >= 8192 && a.N <= 16384);
+  return a.M <= 56 && a.K >= 8192 && a.N >= 32768;
+}
+
+// The split-K kernel runs where it is wanted and its plan either does not
+// split (S = 1: no workspace, the same kernel with or without one given) or
+// a workspace is given.
+bool splitk_selected(const GemmArgs &a, bool have_ws) {
+  if (!splitk_wanted(a) || !splitk_supported(a)) return false;
+  const SplitkPlan p = splitk_plan(a.M, a.N, a.K, false, true);
+  return p.ok && (p.S == 1 || have_ws);
+}
+
 int select_variant(const GemmArgs &a, bool have_ws) {
   if (a.K == 0) return RA_VARIANT_GENERIC;
   // M = 2 runs the small-batch kernels where they apply: the row GEMV
@@ -102,19 +143,11 @@ int select_variant(const GemmArgs &a, bool have_ws) {
     const int v = one_row_short_k(a);
     return v ? v : RA_VARIANT_ROWS;
   }
-  // M = 33..64 with at least 8192 weight rows: the 64-row tiles (K split
-  // over workgroups where that pays), also at long K (M=64 K=28672 N=8192:
-  // 58.0 us against 65.9 for the split-K kernel).
+  // Split K where it is measured ahead (see splitk_wanted), then at M =
+  // 33..64 with at least 8192 weight rows the 64-row tiles (K split over
+  // workgroups where that pays).
+  if (splitk_selected(a, have_ws)) return RA_VARIANT_SPLITK;
   if (tiled_small_selected(a) && !short_k_batch(a)) return RA_VARIANT_TILED;
-  // Split K: long K, or from 16 rows K >= 11008 over at most 4096 weight
-  // rows (M=64 K=14336 N=4096: 29.1 us against 55.0 for the small-batch
-  // kernel, M=16 K=11008 N=4096 15.0 against 16.3).
-  // Only where the plan does split (S > 1): with S = 1 the problem needs no
-  // workspace, and a call with one must run what a call without one runs.
-  if (have_ws && a.M <= kSkinnyMaxM && splitk_supported(a) &&
-      (a.K >= kSplitkMinK || (a.M >= 16 && a.K >= 11008 && a.N <= 4096)) &&
-      splitk_plan(a.M, a.N, a.K, false, true).S > 1)
-    return RA_VARIANT_SPLITK;
   // The split-K kernel without a split (S = 1, no workspace, with or
   // without one given) at M = 17..32, K = 2048..4096 over 28672+ weight
   // rows, where the small-batch kernel needs a second round of workgroups
@@ -186,6 +219,7 @@ void ra_tune_batch_xlds(int v) { ra::g_batch_xlds = v; }
 void ra_tune_batch_xd(int v) { ra::g_batch_xd = v; }
 void ra_tune_sk(int s, int dmax) { ra::g_sk_s = s; ra::g_sk_dmax = dmax; }
 void ra_tune_sk_x1(int off) { ra::g_sk_x1 = off; }
+void ra_tune_sk_tw(int tw) { ra::g_sk_tw = tw; }
 void ra_tune_tiled_split(int v) { ra::g_tiled_split = v; }
 void ra_tune_w8a8(int mode) { ra::g_w8a8_mode = mode; }
 void ra_tune_rows_lds(int v) { ra::g_rows_lds = v; }

@@ -96,6 +96,9 @@ hipError_t gateup_batch_launch(const GateUpArgs &a, hipStream_t s);
 // Bytes of the counter block at the start of every split-K workspace (must
 // be zero before the first use; each call leaves it zero).
 constexpr size_t kSplitkCounterBytes = RA_WORKSPACE_COUNTER_BYTES;  // 4096 counters
+// Largest split-K workspace a plan may use (counters + partial sums); plans
+// that would need more split less.
+constexpr size_t kSplitkMaxWorkspace = (size_t)16 << 20;
 struct SplitkPlan {
   bool ok;
   int mt, tw, S, kc, nb;

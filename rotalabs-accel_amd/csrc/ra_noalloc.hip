@@ -22,6 +22,7 @@
 namespace {
 
 constexpr size_t kScratchBytes = (size_t)16 << 20;  // largest workspace a call may need
+static_assert(kScratchBytes >= ra::kSplitkMaxWorkspace, "every split-K plan fits the array");
 constexpr int kMaxDevices = 64;
 
 }  // namespace
@@ -67,7 +68,7 @@ extern "C" int ra_w8a16_gemm_noalloc(const void *x, int64_t ldx, int x_dtype, co
   if (M == 0 || N == 0) return ra_w8a16_gemm_ws(x, ldx, x_dtype, w, ldw, scale, bias, bias_dtype, y, ldy, M, N, K,
                                                 nullptr, 0, stream);
   size_t need = (x_dtype == RA_F16 || x_dtype == RA_BF16) ? ra::auto_workspace_bytes(a) : 0;
-  if (need > kScratchBytes) {
+  if (need > kScratchBytes) {  // only a tiled split plan can need more (split-K plans are capped)
     if (!ra::auto_workspace_optional(a)) return RA_ERR_WORKSPACE;
     need = 0;  // the tiled kernel runs its tile over all of K instead
   }

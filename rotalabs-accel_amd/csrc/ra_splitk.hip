@@ -41,7 +41,7 @@
 
 namespace ra {
 #ifdef RA_TUNING
-extern int g_sk_s, g_sk_dmax, g_sk_x1;  // tuning builds: forced split count, depth cap, extra-row form
+extern int g_sk_s, g_sk_dmax, g_sk_x1, g_sk_tw;  // tuning builds: forced split count, depth cap, extra-row form, tiles per wave
 #endif
 
 namespace sk {
@@ -240,7 +240,14 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
       for (int t = 0; t < NTW; ++t) {
         const uint2 a8 = *reinterpret_cast<const uint2 *>(ws + (16 * t + r) * 128 +
                                                           (((2 * q + (g >> 1)) ^ wsw) << 4) + 8 * (g & 1));
-        const uint4 a = A::dq8s(a8.x, a8.y);
+        // The compiler-visible dequantiser (for fp16 the magic-number form, not
+        // the SDWA inline assembly of dq8s): with dq8s the fp16 kernel with
+        // one 16-row tile, the extra row and two weight tiles per wave
+        // (MT=1, X1=1, NTW=2) gave wrong sums in rows 0..16 (32171 of
+        // 102000 outputs at M=17 K=16384 N=6000, any split count, also in
+        // the gate/up form), every other instantiation exact; with dq8 all
+        // are exact.
+        const uint4 a = A::dq8(a8.x, a8.y);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[t][mt] = A::mfma16(a, xf[mt], acc[t][mt]);
         if constexpr (X1 != 0) acc1[t] = A::dot8(a, x1f, acc1[t]);
@@ -425,10 +432,28 @@ int device_cus() {
 
 }  // namespace
 
-// Plan: tiles per wave TW and splits S minimising the bytes the busiest CU
-// moves (one workgroup per CU: rounds x per-unit bytes), per unit
-// weight rows x kc + min(M, 16*MT) x kc x 2 activation bytes (+ the partial
-// sums written and, by one unit in S, read back when S > 1).
+// Plan: tiles per wave TW and splits S minimising a time model of the
+// busiest CU. Every split of a row block runs on the row block's XCD
+// (workgroup b on XCD b % 8), so the busiest XCD holds ceil(nb / 8) * S
+// units and its busiest CU n = ceil(that / (CUs / 8)) of them, up to `cap`
+// resident at a time (LDS per workgroup). The CU streams at a fixed share of
+// HBM (~28 GB/s) unless its j = min(n, cap) resident units keep too few
+// weight bytes in flight (D stages of weight copies each) to cover the
+// memory latency; its time is n x the unit's bytes (weight rows x kc,
+// activation rows x kc x 2 at about half weight (they come from L2), the
+// fp32 partial sums written and read back when S > 1) over that rate, plus
+// a fixed cost per round of resident units (pipeline fill and drain), plus
+// the combining unit's serial read of the other S - 1 splits' partial sums.
+// The constants are a least-squares fit to 1279 timed plans (every TW x S
+// at 38 shapes, M = 2..64, K = 2048..28672, N = 2048..57344; relative rms
+// error 10 %): over those shapes the model's pick is 1.5 % slower than the
+// fastest plan on average (11 % at worst, the same with each shape left out
+// of the fit), against 29 % (88 %) for the former bytes-per-round model, which
+// counted rounds over all CUs instead of the busiest XCD's (nb = 27, S = 9:
+// 243 units for 256 CUs, but 36 on the 32 CUs of three XCDs) and had no
+// latency bound. Splits whose partial sums exceed kSplitkMaxWorkspace are
+// not considered (at M=32 K=28672 N=32768 a 5-way split of 192-row blocks,
+// 21 MB of partial sums, measured 196.7 us against 171.7 unsplit).
 SplitkPlan splitk_plan(int64_t M, int64_t N, int64_t K, bool gu, bool allow_split) {
   SplitkPlan best{};
   best.ok = false;
@@ -443,30 +468,47 @@ SplitkPlan splitk_plan(int64_t M, int64_t N, int64_t K, bool gu, bool allow_spli
     x1 = 1;
   }
   const int cus = device_cus();
+  const int64_t xcd_cus = std::max(cus / 8, 1);
   const int64_t stages = K / sk::KS;
+  constexpr int kCuLds = 160 * 1024;
+  // Fitted: CU share of HBM (bytes/us), memory latency (us), cost per round
+  // (us), activation and partial-sum byte weights, and the combining unit's
+  // read of the other splits' partial sums (us per byte).
+  constexpr double kCuRate = 27.81e3, kLatency = 1.112, kRound = 1.167, kActW = 0.508, kPartW = 1.681,
+                   kCombine = 0.03768e-3;
   double best_t = 0;
-  int force_s = 0;
+  int force_s = 0, force_tw = 0;
 #ifdef RA_TUNING
   force_s = g_sk_s;
+  force_tw = g_sk_tw;
 #endif
   for (int tw = 1; tw <= 3; ++tw) {
+    if (force_tw > 0 && tw != force_tw) continue;
     const int ntw = gu ? 2 * tw : tw;
     const int64_t R = (int64_t)sk::NW * tw * 16;
     const int64_t nb = (N + R - 1) / R;
     const int smax = (allow_split && nb <= sk::kMaxCounters) ? (int)std::min<int64_t>(stages, 16) : 1;
+    const int d = sk::depth(mt, tw, gu, sk::kMaxD, x1);
+    const int lds = sk::lds_bytes(mt, tw, gu, d, x1) + 4;  // + the flag
+    const int64_t cap = std::max(kCuLds / ((lds + 511) / 512 * 512), 1);  // resident units per CU
+    const double inflight = (double)d * ntw * 16 * sk::NW * sk::KS;  // weight bytes in flight per unit
     for (int S = 1; S <= smax; ++S) {
       if (force_s > 0 && S != force_s) continue;
       const int64_t kst = (stages + S - 1) / S;  // stages per split
       const int64_t se = (stages + kst - 1) / kst;
       if (se != S) continue;                     // a split would be empty
       const int64_t kc = kst * sk::KS;
-      const int64_t units = nb * S;
+      if (S > 1 && sk::kCounterBytes + (size_t)S * nb * sk::part_floats(mt, tw, gu, x1) * 4 > kSplitkMaxWorkspace)
+        continue;  // partial sums beyond the workspace limit
       const int64_t slots = ((nb + 7) / 8) * 8 * S;  // grid (XCD-grouped row blocks)
-      const int64_t rounds = (units + cus - 1) / cus;
+      const int64_t n = (((nb + 7) / 8) * S + xcd_cus - 1) / xcd_cus;  // units on the busiest CU
+      const int64_t rounds = (n + cap - 1) / cap;
       const double wbytes = (double)(ntw * 16 * sk::NW) * kc;
       const double xbytes = (double)std::min<int64_t>(M, 16 * mt + x1) * kc * 2;
       const double pbytes = S > 1 ? (double)sk::part_floats(mt, tw, gu, x1) * 4 * (1.0 + 1.0) : 0.0;
-      const double t = (double)rounds * (wbytes + xbytes + pbytes) + 1e-3 * (double)slots;
+      const double rate = std::min(kCuRate, (double)std::min(n, cap) * inflight / kLatency);
+      const double t = (double)n * (wbytes + kActW * xbytes + kPartW * pbytes) / rate + (double)rounds * kRound +
+                       kCombine * (S - 1) * sk::part_floats(mt, tw, gu, x1) * 4 + 1e-6 * (double)slots;
       if (!best.ok || t < best_t) {
         best = SplitkPlan{true, mt, tw, S, (int)kc, (int)nb, false, 0, 0, x1};
         best_t = t;

@@ -66,11 +66,16 @@ def test_argument_checks_without_device_work():
     assert lib.ra_w8a16_gemm_workspace_size(1, 11008, 4096, 0) == 0      # row GEMV: none
     assert lib.ra_w8a16_gemm_workspace_size(2048, 11008, 4096, 0) == 0   # tiled: none
     assert lib.ra_w8a16_gateup_swiglu_ws(n, 0, 0, n, 0, n, n, 0, 0, 8, 8, n, 0, n) == 0
-    # the no-allocation entry point refuses a problem whose split-K workspace exceeds its
-    # 16 MiB array (M=32 K=16384 N=57344 needs ~35 MB) before any launch; argument errors as usual
-    assert lib.ra_w8a16_gemm_select(32, 57344, 16384, 0) == 7
-    assert lib.ra_w8a16_gemm_workspace_size(32, 57344, 16384, 0) > 16 << 20
-    assert lib.ra_w8a16_gemm_noalloc(p, 16384, 0, p, 16384, p, n, 0, p, 57344, 32, 57344, 16384, n) == 6
+    # split-K plans keep their partial sums within the no-allocation entry point's 16 MiB
+    # array: the widest problems split less (or not at all) instead of being refused there
+    # (at M <= 32 the reported size is the split-K plan's; from M = 33 it also covers the
+    # 64-row tiles' split plan, which runs unsplit when the array is too small)
+    for (M, N, K) in [(32, 57344, 16384), (17, 57344, 32768), (32, 32768, 28672), (8, 65536, 16384),
+                      (16, 128256, 16384), (5, 1000, 16384), (24, 28672, 28672)]:
+        assert lib.ra_w8a16_gemm_select(M, N, K, 0) == 7
+        assert 0 <= lib.ra_w8a16_gemm_workspace_size(M, N, K, 0) <= 16 << 20
+    for (M, I, K) in [(64, 28672, 16384), (32, 57344, 28672), (17, 6656, 16384)]:
+        assert lib.ra_w8a16_gateup_workspace_size(M, I, K, 0) <= 16 << 20
     assert lib.ra_w8a16_gemm_noalloc(n, 0, 0, n, 0, n, n, 0, n, 0, -1, 4, 4, n) == 1
     assert lib.ra_w8a16_gemm_noalloc(n, 0, 0, n, 0, n, n, 0, n, 0, 0, 4, 4, n) == 0
 
@@ -87,7 +92,8 @@ def test_variant_selection_fallbacks():
     assert lib.ra_w8a16_gemm_select(17, 8192, 28672, 1) == 7  # ... with K >= 16384: split K over workgroups
     assert lib.ra_w8a16_gemm_select(16, 4096, 11008, 1) == 7  # ... from 16 rows, K >= 11008 over N <= 4096
     assert lib.ra_w8a16_gemm_select(15, 4096, 11008, 1) == 6
-    assert lib.ra_w8a16_gemm_select(16, 4097, 11008, 1) == 6
+    assert lib.ra_w8a16_gemm_select(16, 4097, 11008, 1) == 7  # ... and over more rows from K = 11008
+    assert lib.ra_w8a16_gemm_select(16, 8192, 8192, 1) == 6   # below that the small-batch kernel
     assert lib.ra_w8a16_gemm_select(64, 8192, 28672, 1) == 2  # M = 33..64, N >= 8192: 64-row tiles
     assert lib.ra_w8a16_gemm_select(4, 8192, 1040, 1) == 1   # K % 128 != 0: split-K MFMA kernel
     assert lib.ra_w8a16_gemm_select(1, 64, 50, 0) == 3     # K % 16 != 0 -> generic
@@ -104,7 +110,16 @@ def test_variant_selection_fallbacks():
     (48, 9216, 2048, 2), (33, 13824, 2048, 2), (64, 8192, 2048, 2), (33, 11008, 4096, 2),
     # M = 17..32, K = 2048..4096 over 28672+ rows: the split-K kernel without a split (no workspace)
     (32, 28672, 4096, 7), (17, 28672, 4096, 7), (20, 40960, 2048, 7), (24, 24576, 4096, 6),
-    (32, 27648, 5120, 6), (16, 28672, 4096, 6)])
+    (16, 28672, 4096, 6),
+    # M = 2..32 from K = 5120: split K over 14336+ rows, from 16 rows at K >= 11008, from 24 rows
+    # over at most 4096 rows, at 32 rows; the small-batch kernel below that
+    (32, 27648, 5120, 7), (2, 28672, 5120, 7), (8, 14336, 8192, 7), (16, 8192, 11008, 7),
+    (24, 4096, 8192, 7), (32, 8192, 5120, 7), (8, 8192, 8192, 6), (24, 8192, 8192, 6), (2, 4096, 14336, 6),
+    # M = 33..64: split K from K = 14336 (not at M > 56 over 8192..16384 rows), from K = 8192 over
+    # 32768+ rows, over at most 4096 rows from K = 4096; else the 64-row tiles
+    (33, 16384, 16384, 7), (48, 8192, 28672, 7), (64, 32768, 16384, 7), (40, 32768, 8192, 7),
+    (64, 4096, 8192, 7), (64, 16384, 16384, 2), (64, 8192, 28672, 2), (40, 16384, 8192, 2),
+    (48, 16384, 4096, 2)])
 def test_variant_selection_short_k_and_wide(M, N, K, expect):
     lib = _backend.load()
     assert lib.ra_w8a16_gemm_select(M, N, K, 1) == expect
@@ -188,14 +203,14 @@ def test_misaligned_workspace_refused_before_any_launch():
 
 def test_select_agrees_with_the_workspace_size():
     """Where the split-K plan does not split (S = 1) the problem needs no
-    workspace, so the automatic selection must not pick the split-K kernel
-    either: a call with a workspace then runs what a call without one runs
-    (M=8 K=16384 N=65536, M=2 K=16384 N=128256). Where it does split, select
-    reports split K and the size is non-zero."""
+    workspace: the split-K kernel runs unsplit with or without one given, so
+    a call with a workspace runs what a call without one runs (M=8 K=16384
+    N=65536, M=2 K=16384 N=128256; bitwise in tests/test_gpu_gemm.py). Where
+    it does split, select reports split K and the size is non-zero."""
     lib = _backend.load()
     for (M, N, K) in ((8, 65536, 16384), (2, 128256, 16384)):
         assert lib.ra_w8a16_gemm_workspace_size(M, N, K, 1) == 0
-        assert lib.ra_w8a16_gemm_select(M, N, K, 1) != 7
+        assert lib.ra_w8a16_gemm_select(M, N, K, 1) == 7
     for (M, N, K) in ((17, 8192, 28672), (8, 16384, 16384), (16, 4096, 11008)):
         assert lib.ra_w8a16_gemm_select(M, N, K, 1) == 7
         assert lib.ra_w8a16_gemm_workspace_size(M, N, K, 1) > _backend.WORKSPACE_COUNTER_BYTES

@@ -383,6 +383,37 @@ def test_selection_rule_shapes_exact_and_oracle(gpu, M, K, N, dt):
     _oracle_check(y1.cpu(), c.x, c.q, c.s)
 
 
+# Shapes the split-K selection rules send to the split-K kernel (M = 2..32 from
+# K = 5120 over 14336+ rows, from 16 rows at K >= 11008, from 24 rows over at
+# most 4096 rows, M = 32; M = 33..64 from K = 14336, over at most 4096 rows
+# from K = 4096; K >= 16384), with the plans the time model picks there.
+SPLITK_RULE_SHAPES = [(2, 5120, 14400), (16, 11008, 6000), (24, 5120, 4000), (32, 5120, 6000), (40, 4096, 4000),
+                      (48, 14336, 5000), (4, 16384, 4800), (64, 4096, 4096)]
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M,K,N", SPLITK_RULE_SHAPES)
+def test_splitk_rule_shapes_exact_and_oracle(gpu, M, K, N, dt):
+    """The automatic pick is the split-K kernel: exact known answers
+    (automatic and forced), then two calls in a row on random inputs,
+    bitwise repeatable and, where the oracle is quick, within its bound."""
+    lib = _backend.load()
+    assert lib.ra_w8a16_gemm_select(M, N, K, _backend.dtype_code(dt)) == SPLITK
+    print(f"  split-K rule M={M} K={K} N={N} {dt} workspace "
+          f"{lib.ra_w8a16_gemm_workspace_size(M, N, K, _backend.dtype_code(dt))} B", flush=True)
+    x, q, s, b, exact = _exact_case(M, K, N, dt, seed=3 * M + K + N, dev=gpu, bias=(N % 2 == 0))
+    for v in (0, SPLITK):
+        y = _run(x, q, s, b, v).cpu()
+        assert torch.equal(y, exact.to(dt)), f"variant {v}: max err {(y.double() - exact).abs().max()}"
+    c = gemm_case(M, K, N, seed=M + 11, dtype=dt, outlier_rows=True)
+    xg, qg, sg = c.x.to(gpu), c.q.to(gpu), c.s.to(gpu)
+    y1 = _run(xg, qg, sg, None, 0)
+    y2 = _run(xg, qg, sg, None, 0)
+    assert torch.equal(y1, y2)
+    if K * N <= 4096 * 11008 and M * K * N <= 64 * 4096 * 11008:
+        _oracle_check(y1.cpu(), c.x, c.q, c.s)
+
+
 def test_splitk_plans_share_one_workspace(gpu):
     """Calls with different split plans (58 row blocks x 4 splits, then 94 x
     2, then 4 x 16) on one stream share its workspace: the counters sit in a
@@ -405,7 +436,9 @@ def test_splitk_selected_for_long_k():
     # M = 33..64 with >= 8192 weight rows: the tiled kernel's 64 x 64 tile
     for M in (33, 64):
         assert lib.ra_w8a16_gemm_select(M, 11008, 4096, _backend.F16) == TILED
-    assert lib.ra_w8a16_gemm_select(64, 4096, 4096, _backend.F16) == BATCH
+    # from 24 rows over at most 4096 weight rows: split K (M = 64 from K = 4096)
+    assert lib.ra_w8a16_gemm_select(64, 4096, 4096, _backend.F16) == SPLITK
+    assert lib.ra_w8a16_gemm_select(24, 4096, 4096, _backend.F16) == BATCH
 
 
 def test_two_rows_take_the_small_batch_kernels():

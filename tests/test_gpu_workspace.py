@@ -151,6 +151,73 @@ def test_gateup_splitk_vs_exact_and_oracle(gpu, dt, M, K, inter):
     _check_chain(hr, y64[:, :inter], y64[:, inter:], dt, slack[:, :inter], slack[:, inter:])
 
 
+# One problem per split-K kernel instantiation (GEMM / gate-up, 16*MT-row
+# tiles, the extra row, TW weight tiles per wave), with the plan (TW, S) the
+# time model picks for it, pinned through the workspace size the plan needs.
+SPLITK_INSTANCES = [
+    # (gate/up, M, K, N or I, TW, S)
+    (False, 3, 16384, 256, 1, 16), (False, 8, 16384, 4672, 2, 6), (False, 8, 16384, 8256, 3, 5),
+    (False, 17, 16384, 256, 1, 16), (False, 17, 16384, 2624, 2, 10), (False, 17, 16384, 8256, 3, 5),
+    (False, 18, 16384, 256, 1, 16), (False, 18, 16384, 4672, 2, 6), (False, 18, 16384, 8256, 3, 5),
+    (False, 33, 16384, 256, 1, 13), (False, 33, 16384, 3136, 2, 8), (False, 33, 16384, 8256, 3, 5),
+    (False, 34, 16384, 256, 1, 10), (False, 34, 16384, 4160, 2, 6), (False, 34, 16384, 10304, 3, 4),
+    (True, 3, 16384, 256, 1, 16), (True, 5, 16384, 9792, 2, 3), (True, 8, 16384, 8256, 3, 5),
+    (True, 17, 16384, 256, 1, 13), (True, 17, 16384, 5184, 2, 5), (True, 17, 16384, 8256, 3, 5),
+    (True, 18, 16384, 256, 1, 13), (True, 18, 16384, 5184, 2, 5), (True, 18, 20480, 8256, 3, 5),
+    (True, 33, 16384, 256, 1, 10), (True, 33, 16384, 5184, 2, 5), (True, 33, 20480, 8256, 3, 5),
+    (True, 34, 16384, 256, 1, 8), (True, 34, 16384, 5184, 2, 5)]
+# (gate/up with 64-row tiles and three tiles per wave is never planned: its
+# partial sums exceed the 16 MiB workspace limit wherever it would be picked)
+
+
+def _splitk_ws_bytes(gu, M, K, N, tw, S):
+    """Workspace of split-K plan (tw, S): the counter block, then S fp32
+    partial-sum blocks per row block of 64*tw output columns (4 waves of
+    NTW*MT fragments of 256 floats, plus one group for the extra row)."""
+    x1 = 1 if M in (17, 33) else 0
+    mt = M // 16 if x1 else (1 if M <= 16 else (2 if M <= 32 else 4))
+    ntw = 2 * tw if gu else tw
+    part = 4 * (ntw * mt + x1 * ((ntw + 3) // 4)) * 256
+    return _backend.WORKSPACE_COUNTER_BYTES + S * (-(-N // (64 * tw))) * part * 4
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("gu,M,K,N,tw,S", SPLITK_INSTANCES)
+def test_splitk_every_instantiation_exact(gpu, dt, gu, M, K, N, tw, S):
+    """Exact known answers from every split-K instantiation the library
+    dispatches (both dtypes, GEMM and gate/up): x in {-1, 0, 1} with at most
+    ~200 non-zeros per row and q in [-lim, lim] keep every sum an integer
+    below 2^11, exact in fp32 whatever the order, so any tile, extra-row,
+    split or combine mistake is a mismatch. The inputs are generated and the
+    exact sums formed on the GPU (fp32 products of small integers)."""
+    lib = _backend.load()
+    dcode = _backend.dtype_code(dt)
+    size = lib.ra_w8a16_gateup_workspace_size(M, N, K, dcode) if gu else \
+        lib.ra_w8a16_gemm_workspace_size(M, N, K, dcode)
+    want = _splitk_ws_bytes(gu, M, K, N, tw, S)
+    # (from M = 33 over 8192+ rows the reported size also covers the 64-row
+    # tiles' split plan, which can need more)
+    assert size == want or (not gu and M > 32 and N >= 8192 and size > want), "the plan is not (TW, S)"
+    print(f"  split-K instance gu={gu} M={M} K={K} N={N} tw={tw} S={S} {dt}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(M * 3 + K + N)
+    lim = 3 if dt == torch.float16 else 1
+    rows = 2 * N if gu else N
+    x = torch.randint(-1, 2, (M, K), device=gpu, generator=g).float()
+    x = x * (torch.rand(M, K, device=gpu, generator=g) < 200.0 / K)
+    q = torch.randint(-lim, lim + 1, (rows, K), device=gpu, generator=g, dtype=torch.int8)
+    s = torch.full((rows,), 2.0 ** -4, device=gpu)
+    sums = ((x @ q.float().T) * 2.0 ** -4).double().cpu()
+    if gu:
+        h = ra.int8_gateup_swiglu(x.to(dt), q, s)
+        torch.cuda.synchronize()
+        zero = torch.zeros(M, N, dtype=torch.float64)
+        _check_chain(h.cpu(), sums[:, :N], sums[:, N:], dt, zero, zero)
+        return
+    assert lib.ra_w8a16_gemm_select(M, N, K, dcode) == _backend.VARIANT_SPLITK
+    y = ra.int8_gemm(x.to(dt), q, s).cpu()
+    assert torch.equal(y, sums.to(dt)), f"{int((y.double() != sums).sum())} outputs differ"
+
+
 def _int8_case(M, K, N, dt, seed, dev):
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(M, K, generator=g).to(dt)
@@ -164,7 +231,7 @@ def test_graph_capture_workspaces(gpu):
     each calling kernels that split K through a workspace: graph A (M=17
     K=28672 N=8192, split-K), then graph B (M=5 K=16384 N=1000 split-K, the
     tiled split plan at M=64 K=11008 N=8192 and the gate/up split-K kernel at
-    M=20 I=3000 K=16384, each needing a larger workspace than the one before).
+    M=40 I=6000 K=16384, each needing a larger workspace than the one before).
     B is replayed before A ever ran, then A, then eager calls, then both again
     in the other order; every output of every replay is bitwise equal to the
     eager result (the same kernels in the same order)."""
@@ -174,14 +241,14 @@ def test_graph_capture_workspaces(gpu):
     b1_case = _int8_case(5, 16384, 1000, dt, 2, gpu)
     b2_case = _int8_case(64, 11008, 8192, dt, 3, gpu)
     g = torch.Generator().manual_seed(4)
-    gu_x = torch.randn(20, 16384, generator=g).to(dt).to(gpu)
-    gu_q, gu_s = ra.quantize_weight_per_channel(torch.randn(6000, 16384, generator=g).to(gpu) * 0.02)
+    gu_x = torch.randn(40, 16384, generator=g).to(dt).to(gpu)
+    gu_q, gu_s = ra.quantize_weight_per_channel(torch.randn(12000, 16384, generator=g).to(gpu) * 0.02)
     assert lib.ra_w8a16_gemm_select(17, 8192, 28672, 1) == _backend.VARIANT_SPLITK
     assert lib.ra_w8a16_gemm_select(5, 1000, 16384, 1) == _backend.VARIANT_SPLITK
     assert lib.ra_w8a16_gemm_select(64, 8192, 11008, 1) == _backend.VARIANT_TILED
     sizes = [lib.ra_w8a16_gemm_workspace_size(5, 1000, 16384, 1),
              lib.ra_w8a16_gemm_workspace_size(64, 8192, 11008, 1),
-             lib.ra_w8a16_gateup_workspace_size(20, 3000, 16384, 1)]
+             lib.ra_w8a16_gateup_workspace_size(40, 6000, 16384, 1)]
     assert 0 < sizes[0] < sizes[1] < sizes[2], sizes
 
     def run_a():
@@ -235,12 +302,13 @@ def test_graph_capture_workspaces(gpu):
 
 @pytest.mark.parametrize("M,N,K", [(8, 65536, 16384), (2, 128256, 16384)])
 def test_workspace_call_runs_the_selected_kernel(gpu, M, N, K):
-    """Shapes where the split-K plan would not split (S = 1): no workspace is
-    asked for and the selection is not split K, so ra_w8a16_gemm_ws with a
-    workspace and ra_w8a16_gemm without one produce the same bits."""
+    """Shapes where the split-K plan does not split (S = 1): no workspace is
+    asked for and the split-K kernel runs unsplit with or without one, so
+    ra_w8a16_gemm_ws with a workspace and ra_w8a16_gemm without one produce
+    the same bits."""
     lib = _backend.load()
     assert lib.ra_w8a16_gemm_workspace_size(M, N, K, 0) == 0
-    assert lib.ra_w8a16_gemm_select(M, N, K, 0) != _backend.VARIANT_SPLITK
+    assert lib.ra_w8a16_gemm_select(M, N, K, 0) == _backend.VARIANT_SPLITK
     print(f"  ws vs no ws M={M} N={N} K={K}", flush=True)
     g = torch.Generator(device=gpu).manual_seed(M)
     x = torch.randn(M, K, device=gpu, generator=g).half()
