@@ -32,6 +32,7 @@ int g_sk_x1 = 0;
 int g_sk_tw = 0;
 int g_tiled_split = 0;
 int g_w8a8_mode = 0;
+int g_gu_splitk = 0;
 int g_rows_lds = 0;
 }
 #endif
@@ -131,6 +132,22 @@ bool splitk_selected(const GemmArgs &a, bool have_ws) {
   return p.ok && (p.S == 1 || have_ws);
 }
 
+// The gate/up + SwiGLU product through the split-K kernel (same run, bf16,
+// us, the one-pass gate/up kernels -> split K): K >= 16384; M = 33..64,
+// where the one-pass kernels take two passes over the rows (M=33 K=8192
+// I=28672 169.1 -> 109.2, M=64 235.9 -> 115.9, M=40 K=4096 I=14336 60.8 ->
+// 34.0, M=64 K=3584 I=18944 83.2 -> 59.5), except below M = 48 over at most
+// 4096 gate rows at K < 8192 (M=33 K=4096 I=1792 14.9 against 16.7); from
+// K = 8192 over at most 4096 gate rows, where the one-pass kernels leave CUs
+// idle (M=2 K=8192 I=3584 29.3 -> 16.1, M=32 K=12288 I=4096 71.2 -> 25.5).
+// Below that the one-pass kernels stay ahead (M=17 K=8192 I=28672 79.2
+// against 90.5, M=2 K=4096 I=11008 18.0 against 24.7).
+bool gateup_splitk_wanted(int64_t M, int64_t I, int64_t K) {
+  if (M < 2 || M > kSkinnyMaxM) return false;
+  if (K >= kSplitkMinK || (K >= 8192 && I <= 4096)) return true;
+  return M > 32 && (I > 4096 || M >= 48);
+}
+
 int select_variant(const GemmArgs &a, bool have_ws) {
   if (a.K == 0) return RA_VARIANT_GENERIC;
   // M = 2 runs the small-batch kernels where they apply: the row GEMV
@@ -223,6 +240,7 @@ void ra_tune_sk_tw(int tw) { ra::g_sk_tw = tw; }
 void ra_tune_tiled_split(int v) { ra::g_tiled_split = v; }
 void ra_tune_w8a8(int mode) { ra::g_w8a8_mode = mode; }
 void ra_tune_rows_lds(int v) { ra::g_rows_lds = v; }
+void ra_tune_gu_splitk(int v) { ra::g_gu_splitk = v; }
 #endif
 #ifdef RA_TRACE
 // Trace builds only: device buffer for the tiled kernel's per-workgroup timestamps (NULL: none).
@@ -325,8 +343,8 @@ int ra_w8a16_gemm_select(int64_t M, int64_t N, int64_t K, int x_dtype) {
 
 size_t ra_w8a16_gateup_workspace_size(int64_t M, int64_t I, int64_t K, int x_dtype) {
   if (x_dtype != RA_F16 && x_dtype != RA_BF16) return 0;
-  // Only the split-K gate/up kernel uses a workspace, from K = kSplitkMinK.
-  if (M < 2 || M > kSkinnyMaxM || K < kSplitkMinK) return 0;
+  // Only the split-K gate/up kernel uses a workspace, where it is selected.
+  if (!gateup_splitk_wanted(M, I, K) || K < 128 || K % 128 != 0) return 0;
   const SplitkPlan p = splitk_plan(M, I, K, true, true);
   return p.ok ? p.ws_bytes : 0;
 }
@@ -351,9 +369,14 @@ int ra_w8a16_gateup_swiglu_ws(const void *x, int64_t ldx, int x_dtype, const int
   const bool have_ws = workspace != nullptr && workspace_bytes > 0;
   if (K > 0 && gateup_gemv_rows_supported(a) && (M == 1 || !gateup_batch_supported(a)))
     return to_status(gateup_gemv_rows_launch(a, s));
-  if (K >= kSplitkMinK && have_ws && M <= kSkinnyMaxM && gateup_splitk_supported(a)) {
+  bool gu_split = gateup_splitk_wanted(M, I, K);
+#ifdef RA_TUNING
+  if (g_gu_splitk) gu_split = g_gu_splitk > 0;  // tuning builds: 1 forces, -1 forbids the split-K kernel
+#endif
+  // A plan that splits needs the workspace; an unsplit one runs either way.
+  if (gu_split && gateup_splitk_supported(a)) {
     const SplitkPlan p = splitk_plan(M, I, K, true, true);
-    if (p.ok) {
+    if (p.ok && (p.S == 1 || have_ws)) {
       if (p.ws_bytes > 0 && workspace_bytes < p.ws_bytes) return RA_ERR_WORKSPACE;
       return to_status(gateup_splitk_launch(a, p, workspace, s));
     }

@@ -217,10 +217,16 @@ def test_select_agrees_with_the_workspace_size():
 
 
 def test_gateup_workspace_only_where_gateup_splits():
-    """The gate/up kernels split K only from K = 16384; below it the size is 0,
-    so the Python layer allocates no workspace it never uses."""
+    """The gate/up product runs the split-K kernel from K = 16384, at M = 33..64,
+    and from K = 8192 over at most 4096 gate rows; elsewhere the size is 0, so
+    the Python layer allocates no workspace it never uses."""
     lib = _backend.load()
-    assert lib.ra_w8a16_gateup_workspace_size(17, 28672, 8192, 1) == 0
+    assert lib.ra_w8a16_gateup_workspace_size(17, 28672, 8192, 1) == 0     # the one-pass kernels
+    assert lib.ra_w8a16_gateup_workspace_size(32, 14336, 4096, 1) == 0
+    assert lib.ra_w8a16_gateup_workspace_size(8, 4097, 8192, 1) == 0
     assert lib.ra_w8a16_gateup_workspace_size(17, 3000, 16384, 1) > _backend.WORKSPACE_COUNTER_BYTES
-    assert lib.ra_w8a16_gateup_workspace_size(1, 3000, 16384, 1) == 0
+    assert lib.ra_w8a16_gateup_workspace_size(1, 3000, 16384, 1) == 0      # the row GEMV
+    assert lib.ra_w8a16_gateup_workspace_size(48, 3000, 4096, 1) > _backend.WORKSPACE_COUNTER_BYTES
+    assert lib.ra_w8a16_gateup_workspace_size(2, 3584, 8192, 1) > _backend.WORKSPACE_COUNTER_BYTES
+    assert lib.ra_w8a16_gateup_workspace_size(40, 3000, 4160, 1) == 0      # K % 128 != 0
 

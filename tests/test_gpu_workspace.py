@@ -107,10 +107,15 @@ def _check_chain(h, g64, u64, dt, gslack, uslack):
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("M,K,inter", [(17, 16384, 3000), (2, 16384, 700), (64, 32768, 1000), (5, 16384, 48),
-                                        (33, 16384, 520)])
+                                        (33, 16384, 520),
+                                        # below K = 16384: M = 33..64 (from 48 rows or over 4096+ gate rows),
+                                        # and at most 4096 gate rows from K = 8192
+                                        (48, 4096, 3000), (33, 3584, 4200), (64, 8192, 2000), (2, 8192, 3584),
+                                        (24, 12288, 1000)])
 def test_gateup_splitk_vs_exact_and_oracle(gpu, dt, M, K, inter):
-    """The gate/up + SwiGLU GEMM at K >= 16384 splits K over workgroups (a
-    workspace is asked for and given). Exact integer sums make the fp32 gate
+    """The gate/up + SwiGLU GEMM through the split-K kernel (K >= 16384, M =
+    33..64, or at most 4096 gate rows from K = 8192; a workspace is asked for
+    and given). Exact integer sums make the fp32 gate
     and up values order-independent, so the output must be the reference
     composition's roundings of them bit for bit (up to silu's own fp32
     rounding at a boundary), with and without a workspace; a second call on
@@ -128,7 +133,7 @@ def test_gateup_splitk_vs_exact_and_oracle(gpu, dt, M, K, inter):
     assert torch.equal(h1, h2), "second call differs: split counters not reset"
     zero = torch.zeros(M, inter, dtype=torch.float64)
     _check_chain(h1.cpu(), sums[:, :inter], sums[:, inter:], dt, zero, zero)
-    # the same inputs without a workspace (the one-pass kernels)
+    # the same inputs without a workspace (the one-pass kernels, or split K where its plan does not split)
     h0 = torch.empty_like(h1)
     xc = xd.contiguous()
     _backend.check(lib.ra_w8a16_gateup_swiglu(xc.data_ptr(), K, dcode, qd.data_ptr(), K, sd.data_ptr(),
