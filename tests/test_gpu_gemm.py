@@ -602,6 +602,55 @@ def test_empty_and_k_tail(gpu):
             _oracle_check(y.cpu(), c.x, c.q, c.s)
 
 
+def _random_exact_shapes(seed, count):
+    """Seeded (gate/up, M, K, N) over the sizes the selection rules separate:
+    M = 1..512, K = 512..28672 (multiples of 128 and 512 both), N from 64 to
+    28672 (ragged and round)."""
+    import random
+    rng = random.Random(seed)
+    Ms = [1, 2, 3, 4, 5, 7, 8, 12, 16, 17, 18, 24, 31, 32, 33, 40, 48, 56, 63, 64, 65, 96, 128, 200, 256, 512]
+    Ks = [512, 1024, 1536, 2048, 3072, 3584, 4096, 5120, 6144, 8192, 11008, 12288, 14336, 16384, 18944, 28672]
+    out = []
+    while len(out) < count:
+        M, K = rng.choice(Ms), rng.choice(Ks)
+        N = rng.choice([rng.randrange(64, 4096), rng.randrange(4096, 16384), rng.choice([4096, 8192, 11008, 28672])])
+        if M * K <= 32e6 and N * K <= 200e6:
+            out.append((rng.random() < 0.3 and M <= 64, M, K, N))
+    return out
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_exact_random_shapes_automatic_pick(gpu, dt):
+    """Exact known answers through the automatic pick at 120 seeded shapes
+    (GEMM and gate/up + SwiGLU): x in {-1, 0, 1} with ~120 non-zeros per row
+    and small integer weights keep every sum an integer far below 2^11, exact
+    in fp32 in any order, so the GEMM output must equal the rounded sums bit
+    for bit; the gate/up output must match silu(gate) * up on the rounded
+    sums (the reference composition's roundings) within rtol = atol = 1e-2
+    everywhere and bit for bit at all but 0.5 % of the outputs. Inputs and
+    the exact sums are formed on the GPU (fp32 products of small integers)."""
+    for (gu, M, K, N) in _random_exact_shapes(7, 120):
+        print(f"  random exact gu={gu} M={M} K={K} N={N} {dt}", flush=True)
+        g = torch.Generator(device=gpu).manual_seed(M * 7 + K + N)
+        lim = 3 if dt == torch.float16 else 1
+        rows = 2 * N if gu else N
+        x = torch.randint(-1, 2, (M, K), device=gpu, generator=g).float()
+        x = x * (torch.rand(M, K, device=gpu, generator=g) < 120.0 / K)
+        q = torch.randint(-lim, lim + 1, (rows, K), device=gpu, generator=g, dtype=torch.int8)
+        s = torch.full((rows,), 2.0 ** -4, device=gpu)
+        sums = (x @ q.float().T) * 2.0 ** -4
+        if gu:
+            h = ra.int8_gateup_swiglu(x.to(dt), q, s).float()
+            gb, ub = sums[:, :N].to(dt).float(), sums[:, N:].to(dt).float()
+            ref = ((gb * torch.sigmoid(gb)).to(dt).float() * ub).to(dt).float()
+            assert bool(((h - ref).abs() <= 1e-2 + 1e-2 * ref.abs()).all()), f"gate/up M={M} K={K} I={N}"
+            assert float((h != ref).float().mean()) < 5e-3, f"gate/up M={M} K={K} I={N}"
+        else:
+            y = ra.int8_gemm(x.to(dt), q, s).float()
+            want = sums.to(dt).float()
+            assert torch.equal(y, want), f"M={M} K={K} N={N}: {int((y != want).sum())} outputs differ"
+
+
 def test_graph_replay_matches_eager(gpu):
     c = gemm_case(1, 4096, 11008, seed=2, device=gpu)
     eager = ra.int8_gemm(c.x, c.q, c.s)
