@@ -157,11 +157,20 @@ __device__ __forceinline__ uint4 dq8_f16(uint32_t w0, uint32_t w1) {
 // hence the inline assembly; being opaque to the scheduler, it stays out of
 // the tiled GEMM, whose dequantisation is interleaved with the MFMAs by
 // scheduling groups (there it measured 2 % slower).
+// Each pair ends with one wait state (s_nop 0) after the upper-half write:
+// without it the fp16 split-K kernel with one 16-row tile, the extra row and
+// two weight tiles per wave gave wrong sums in rows 0..16 (32171 of 102000
+// outputs at M=17 K=16384 N=6000), while the build that differs only by these
+// nops (the same instruction stream otherwise) is exact. The compiler does not
+// pad after inline assembly the way it pads its own 16-bit partial writes.
+// Cost of the nop: 0.3-1.7 % on the row GEMV, small-batch and 64-row tile
+// kernels (M=1 K=4096 N=11008 8.31 -> 8.34 us).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t cvt2_f16_b01(uint32_t w) {
   uint32_t r;
   asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-      "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1"
+      "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+      "s_nop 0"
       : "=&v"(r)
       : "v"(w));
   return r;
@@ -169,7 +178,8 @@ __device__ __forceinline__ uint32_t cvt2_f16_b01(uint32_t w) {
 __device__ __forceinline__ uint32_t cvt2_f16_b23(uint32_t w) {
   uint32_t r;
   asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
-      "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
+      "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3\n\t"
+      "s_nop 0"
       : "=&v"(r)
       : "v"(w));
   return r;
