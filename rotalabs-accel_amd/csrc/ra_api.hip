@@ -30,6 +30,7 @@ int g_sk_s = 0;
 int g_sk_dmax = 0;
 int g_sk_x1 = 0;
 int g_sk_tw = 0;
+int g_sk_nw = 0;
 int g_tiled_split = 0;
 int g_w8a8_mode = 0;
 int g_gu_splitk = 0;
@@ -165,8 +166,8 @@ int select_variant(const GemmArgs &a, bool have_ws) {
   // workgroups where that pays).
   if (splitk_selected(a, have_ws)) return RA_VARIANT_SPLITK;
   if (tiled_small_selected(a) && !short_k_batch(a)) return RA_VARIANT_TILED;
-  // The split-K kernel without a split (S = 1, no workspace, with or
-  // without one given) at M = 17..32, K = 2048..4096 over 28672+ weight
+  // The split-K kernel (a plan that splits needs the workspace, an unsplit
+  // one runs either way) at M = 17..32, K = 2048..4096 over 28672+ weight
   // rows, where the small-batch kernel needs a second round of workgroups
   // (same run, bf16, us: M=32 K=4096 N=28672 37.9 -> 29.8, M=24 K=3072
   // N=40960 36.3 -> 31.4, M=20 K=2048 N=28672 18.3 -> 17.5, M=17 K=4096
@@ -174,7 +175,7 @@ int select_variant(const GemmArgs &a, bool have_ws) {
   // kernel stays ahead).
   if (a.M >= 17 && a.M <= 32 && a.K >= 2048 && a.K <= 4096 && a.N >= 28672 && splitk_supported(a)) {
     const SplitkPlan p = splitk_plan(a.M, a.N, a.K, false, true);
-    if (p.ok && p.S == 1) return RA_VARIANT_SPLITK;
+    if (p.ok && (p.S == 1 || have_ws)) return RA_VARIANT_SPLITK;
   }
   // M = 3..64: the small-batch kernel (line-wide weight loads, activations
   // read once per 48 rows) where K % 128 == 0, else the split-K MFMA kernel;
@@ -237,6 +238,7 @@ void ra_tune_batch_xd(int v) { ra::g_batch_xd = v; }
 void ra_tune_sk(int s, int dmax) { ra::g_sk_s = s; ra::g_sk_dmax = dmax; }
 void ra_tune_sk_x1(int off) { ra::g_sk_x1 = off; }
 void ra_tune_sk_tw(int tw) { ra::g_sk_tw = tw; }
+void ra_tune_sk_nw(int nw) { ra::g_sk_nw = nw; }
 void ra_tune_tiled_split(int v) { ra::g_tiled_split = v; }
 void ra_tune_w8a8(int mode) { ra::g_w8a8_mode = mode; }
 void ra_tune_rows_lds(int v) { ra::g_rows_lds = v; }

@@ -105,6 +105,7 @@ struct SplitkPlan {
   bool spread;  // a row block's splits on different XCDs (test mode)
   size_t cnt_bytes, ws_bytes;
   int x1;  // 1: M = 16*mt + 1, the last row summed on the VALU
+  int nw;  // waves per workgroup (4)
 };
 SplitkPlan splitk_plan(int64_t M, int64_t N, int64_t K, bool gu, bool allow_split);
 bool splitk_supported(const GemmArgs &a);

@@ -10,9 +10,11 @@
 // S times more rows for the same weight bytes, so it reads S times fewer
 // activation bytes; the S partial sums are combined in a fixed order.
 //
-//  * Unit = (row block rb, K split s); a workgroup of 4 waves owns
-//    R = 4*TW*16 output columns (with the gate/up pair, TW gate tiles and the
-//    TW matching up tiles per wave) over K range [s*kc, min(K, (s+1)*kc)).
+//  * Unit = (row block rb, K split s); a workgroup of NW = 4 or 8 waves owns
+//    R = NW*TW*16 output columns (with the gate/up pair, TW gate tiles and
+//    the TW matching up tiles per wave) over K range [s*kc, min(K, (s+1)*kc)).
+//    With 8 waves two share each SIMD, so one wave's dequantisation, MFMAs
+//    and LDS reads overlap the other's waits.
 //  * Y^T = W . X^T with v_mfma_f32_16x16x32_{f16,bf16}: MFMA rows are weight
 //    rows, MFMA columns activation rows (M padded to 16*MT).
 //  * Both operands reach LDS through direct-to-LDS copies
@@ -24,9 +26,9 @@
 //      its LDS slot), so the MFMA operand reads (16 rows, same chunk) are
 //      conflict-free; the int8 values are dequantised exactly in registers.
 //    - activations: the stage's [16*MT, 128] fp16/bf16 block is copied once
-//      per workgroup (4 rows x 256 bytes per copy, chunks swizzled by
-//      row & 15) into a ring of D+1 slots shared by the 4 waves; one barrier
-//      per stage.
+//      per workgroup (4 rows x 256 bytes per copy, 2 rows when 8 waves share
+//      16 rows; chunks swizzled by row & 15) into a ring of D+1 slots shared
+//      by the waves; one barrier per stage.
 //    No VGPR holds data in flight, so the pipeline depth is set by LDS alone.
 //  * S = 1: the epilogue applies scale (+ bias) or the gate/up SwiGLU to the
 //    fp32 sums and rounds once. S > 1: every unit stores its fp32 partial
@@ -41,7 +43,7 @@
 
 namespace ra {
 #ifdef RA_TUNING
-extern int g_sk_s, g_sk_dmax, g_sk_x1, g_sk_tw;  // tuning builds: forced split count, depth cap, extra-row form, tiles per wave
+extern int g_sk_s, g_sk_dmax, g_sk_x1, g_sk_tw, g_sk_nw;  // tuning builds: forced split count, depth cap, extra-row form, tiles per wave, waves
 #endif
 
 namespace sk {
@@ -63,21 +65,32 @@ constexpr int ntw(int tw, bool gu) { return gu ? 2 * tw : tw; }
 constexpr int x_slot(int mt) { return mt * 4096; }            // [16*MT rows][256 bytes]
 constexpr int w_slot(int tw, bool gu) { return ntw(tw, gu) * 2048; }  // per wave: [16*NTW rows][128 bytes]
 constexpr int x1_slot = 256;                                  // the extra row: [128 k] of 2 bytes
-constexpr int lds_bytes(int mt, int tw, bool gu, int d, int x1 = 0) {
-  return (d + 1) * (x_slot(mt) + x1 * x1_slot) + d * NW * w_slot(tw, gu);
+constexpr int lds_bytes(int mt, int tw, bool gu, int d, int x1 = 0, int nw = NW) {
+  return (d + 1) * (x_slot(mt) + x1 * x1_slot) + d * nw * w_slot(tw, gu);
 }
-constexpr int copies(int mt, int tw, bool gu, int x1 = 0) { return 2 * ntw(tw, gu) + mt + x1; }  // per wave per stage
+// Activation copies per wave per stage and rows per copy: the stage's 16*MT
+// rows of 256 bytes are copied by the nw waves, 4 rows (64 lanes x 16 bytes)
+// per copy, or 2 rows (lanes 0..31) when 8 waves share 16 rows.
+constexpr int xcw(int mt, int nw) { return (4 * mt + nw - 1) / nw; }
+constexpr int rpc(int mt, int nw) { return 16 * mt / (nw * xcw(mt, nw)); }
+constexpr int copies(int mt, int tw, bool gu, int x1 = 0, int nw = NW) {  // per wave per stage
+  return 2 * ntw(tw, gu) + xcw(mt, nw) + x1;
+}
 // Deepest pipeline that fits LDS and the 6-bit vmcnt.
-constexpr int depth(int mt, int tw, bool gu, int dmax = kMaxD, int x1 = 0) {
+constexpr int depth(int mt, int tw, bool gu, int dmax = kMaxD, int x1 = 0, int nw = NW) {
   int d = dmax;
-  while (d > 2 && (lds_bytes(mt, tw, gu, d, x1) > kLds || (d - 1) * copies(mt, tw, gu, x1) > 63)) --d;
+  while (d > 2 && (lds_bytes(mt, tw, gu, d, x1, nw) > kLds || (d - 1) * copies(mt, tw, gu, x1, nw) > 63)) --d;
   return d;
 }
 // fp32 partial sums of one wave per split: NTW x MT fragments of 64 lanes x 4,
 // then (extra row) the NTW row sums per lane, packed 4 to a 16-byte group.
 constexpr int x1_groups(int tw, bool gu) { return (ntw(tw, gu) + 3) / 4; }
 constexpr int wave_floats(int mt, int tw, bool gu, int x1) { return (ntw(tw, gu) * mt + x1 * x1_groups(tw, gu)) * 256; }
-constexpr int part_floats(int mt, int tw, bool gu, int x1 = 0) { return NW * wave_floats(mt, tw, gu, x1); }
+constexpr int part_floats(int mt, int tw, bool gu, int x1 = 0, int nw = NW) { return nw * wave_floats(mt, tw, gu, x1); }
+// The rings fit LDS at the depth chosen.
+constexpr bool fits(int mt, int tw, bool gu, int x1, int nw) {
+  return lds_bytes(mt, tw, gu, depth(mt, tw, gu, kMaxD, x1, nw), x1, nw) <= kLds;
+}
 }  // namespace sk
 
 // Non-temporal direct-to-LDS copy (the weight rows are read once per call).
@@ -103,8 +116,8 @@ __device__ __forceinline__ void wait_stages(int younger) {
 // row is a dot product on the VALU (v_dot2 over the weights the MFMA tiles
 // already dequantised), instead of a second, almost empty 16-row MFMA tile
 // (whose activation copies, LDS reads and MFMAs cost as much as a full one).
-template <int DT, int MT, int TW, bool GU, int X1, int DMAX = sk::kMaxD>
-__global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__ xb, int64_t ldx,
+template <int DT, int MT, int TW, bool GU, int X1, int DMAX = sk::kMaxD, int NWT = sk::NW>
+__global__ __launch_bounds__(64 * NWT, 1) void splitk_kernel(const char *__restrict__ xb, int64_t ldx,
                                                         const char *__restrict__ wb, int64_t ldw,
                                                         const float *__restrict__ scale,
                                                         const void *__restrict__ bias, int bias_dt,
@@ -114,14 +127,18 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
   using A = Act<DT>;
   using namespace sk;
   constexpr int NTW = ntw(TW, GU);
-  constexpr int WL = 2 * NTW;       // weight copies per stage per wave
-  constexpr int CP = WL + MT + X1;  // copies per stage per wave
-  constexpr int D = depth(MT, TW, GU, DMAX, X1);
+  constexpr int WL = 2 * NTW;                              // weight copies per stage per wave
+  constexpr int XCW = xcw(MT, NWT), RPC = rpc(MT, NWT);    // activation copies per wave, rows per copy
+  constexpr int CP = WL + XCW + X1;                        // copies per stage per wave
+  constexpr int D = depth(MT, TW, GU, DMAX, X1, NWT);
   constexpr int XS = x_slot(MT), WS = w_slot(TW, GU);
-  constexpr int XRING = 0, WRING = (D + 1) * XS, X1RING = WRING + D * NW * WS;
-  constexpr int R = NW * TW * 16;  // output columns per unit
+  constexpr int XRING = 0, WRING = (D + 1) * XS, X1RING = WRING + D * NWT * WS;
+  constexpr int R = NWT * TW * 16;  // output columns per unit
+  constexpr int X1L = 16 / NWT;     // lanes per wave copying the extra row (16 bytes each)
   static_assert(X1 == 0 || X1 == 1, "at most one row past the MFMA tiles");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes(MT, TW, GU, D, X1)];
+  static_assert(NWT == 4 || NWT == 8, "4 or 8 waves per workgroup");
+  static_assert(XCW * RPC * NWT == 16 * MT && (RPC == 2 || RPC == 4), "activation copies cover the tile rows");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[lds_bytes(MT, TW, GU, D, X1, NWT)];
   __shared__ int s_last;
 
   // Unit -> (row block, split). Units of one row block are dealt to one XCD
@@ -172,38 +189,46 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
     const int chunk = (lane & 7) ^ ((row >> 1) & 7);
     wvoff[j] = (uint32_t)((int64_t)wrow * ldw + 16 * chunk);
   }
-  // Activation copy c of this wave covers block rows 4i .. 4i+3, i = wid*MT + c;
-  // lane -> row 4i + lane/16, LDS slot lane%16 <- global chunk (lane%16) ^
-  // (row & 15). Rows past M read row M-1 (their columns are never stored).
-  uint32_t xvoff[MT];
+  // Activation copy c of this wave covers block rows RPC*i .. RPC*i+RPC-1,
+  // i = wid*XCW + c (RPC = 4, or 2 with lanes 0..31 when 8 waves share 16
+  // rows); lane -> row RPC*i + lane/16, LDS slot lane%16 <- global chunk
+  // (lane%16) ^ (row & 15). Rows past M read row M-1 (never stored).
+  uint32_t xvoff[XCW];
 #pragma unroll
-  for (int c = 0; c < MT; ++c) {
-    const int row = 4 * (wid * MT + c) + (lane >> 4);
+  for (int c = 0; c < XCW; ++c) {
+    const int row = RPC * (wid * XCW + c) + min(lane >> 4, RPC - 1);
     const int xrow = row < M ? row : M - 1;
     const int chunk = (lane & 15) ^ (row & 15);
     xvoff[c] = (uint32_t)(((int64_t)xrow * ldx + 8 * chunk) * 2);
   }
   const uint32_t lds0 = lds_offset(lds);
   const uint32_t wdst = lds0 + WRING + (uint32_t)wid * WS;
-  const uint32_t xdst = lds0 + XRING + (uint32_t)(wid * MT) * 1024;
-  // Extra row (X1): the stage's 256 bytes of row 16*MT, 64 per wave, copied
-  // by lanes 0..3 (16 bytes each, k = 32*wid + 8*lane .. +7).
-  const uint32_t x1voff = (uint32_t)(((int64_t)(16 * MT) * ldx) * 2 + 64 * wid + 16 * (lane & 3));
-  const uint32_t x1dst = lds0 + X1RING + (uint32_t)(64 * wid);
+  const uint32_t xdst = lds0 + XRING + (uint32_t)(wid * XCW * RPC) * 256;
+  // Extra row (X1): the stage's 256 bytes of row 16*MT, 256/NWT per wave,
+  // copied by lanes 0..X1L-1 (16 bytes each).
+  const uint32_t x1voff =
+      (uint32_t)(((int64_t)(16 * MT) * ldx) * 2 + (256 / NWT) * wid + 16 * (lane & (X1L - 1)));
+  const uint32_t x1dst = lds0 + X1RING + (uint32_t)((256 / NWT) * wid);
 
   auto issue = [&](int st) __attribute__((always_inline)) {
     const int sr = st + rot < nst ? st + rot : st + rot - nst;
     const int k = kb + sr * KS;
     const char *sw = wb + k;
     const char *sx = xb + (int64_t)k * 2;
-    const uint32_t wd = wdst + (uint32_t)((st % D) * NW * WS);
+    const uint32_t wd = wdst + (uint32_t)((st % D) * NWT * WS);
     const uint32_t xd = xdst + (uint32_t)((st % (D + 1)) * XS);
 #pragma unroll
     for (int j = 0; j < WL; ++j) dma16s_nt(sw, wvoff[j], wd + 1024u * j);
 #pragma unroll
-    for (int c = 0; c < MT; ++c) dma16s<0, true>(sx, xvoff[c], xd + 1024u * c);
+    for (int c = 0; c < XCW; ++c) {
+      if constexpr (RPC == 4) {
+        dma16s<0, true>(sx, xvoff[c], xd + 1024u * c);
+      } else {
+        if (lane < 16 * RPC) dma16s<0, true>(sx, xvoff[c], xd + (uint32_t)(RPC * 256) * c);
+      }
+    }
     if constexpr (X1 != 0) {
-      if (lane < 4) dma16s<0, true>(sx, x1voff, x1dst + (uint32_t)((st % (D + 1)) * x1_slot));
+      if (lane < X1L) dma16s<0, true>(sx, x1voff, x1dst + (uint32_t)((st % (D + 1)) * x1_slot));
     }
   };
 
@@ -225,7 +250,7 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
   for (int st = 0; st < nst; ++st) {
     wait_stages<CP, D>(min(D - 1, nst - 1 - st));
     __syncthreads();  // every wave's copies of stage st have landed
-    const uint8_t *ws = lds + WRING + ((st % D) * NW + wid) * WS;
+    const uint8_t *ws = lds + WRING + ((st % D) * NWT + wid) * WS;
     const uint8_t *xs = lds + XRING + (st % (D + 1)) * XS;
     const uint8_t *x1s = lds + X1RING + (st % (D + 1)) * x1_slot;
 #pragma unroll
@@ -274,22 +299,22 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
     // invalidate the whole L2 of the XCD, a cost every unit would pay.
     constexpr int FR = wave_floats(MT, TW, GU, X1);  // floats per wave and split
     constexpr int G1 = x1_groups(TW, GU);
-    // this row block's partial sums: [S][NW][NTW * MT fragments + G1 groups][64 lanes][4]
+    // this row block's partial sums: [S][NWT][NTW * MT fragments + G1 groups][64 lanes][4]
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        part + (size_t)rb * S * NW * FR, 0, (int)(S * NW * FR * sizeof(float)), kRsrcWord3);
+        part + (size_t)rb * S * NWT * FR, 0, (int)(S * NWT * FR * sizeof(float)), kRsrcWord3);
     const uint32_t lo = (uint32_t)(wid * FR + lane * 4) * 4u;  // byte offset of this lane in split 0
 #pragma unroll
     for (int t = 0; t < NTW; ++t)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        store_dev16(rs, lo + (uint32_t)(s * NW * FR + (t * MT + mt) * 256) * 4u, acc[t][mt]);
+        store_dev16(rs, lo + (uint32_t)(s * NWT * FR + (t * MT + mt) * 256) * 4u, acc[t][mt]);
     if constexpr (X1 != 0) {
 #pragma unroll
       for (int q1 = 0; q1 < G1; ++q1) {
         f32x4 e;
 #pragma unroll
         for (int i = 0; i < 4; ++i) e[i] = 4 * q1 + i < NTW ? acc1[4 * q1 + i] : 0.f;
-        store_dev16(rs, lo + (uint32_t)(s * NW * FR + (NTW * MT + q1) * 256) * 4u, e);
+        store_dev16(rs, lo + (uint32_t)(s * NWT * FR + (NTW * MT + q1) * 256) * 4u, e);
       }
     }
     wait_vmcnt<0>();  // this wave's partial sums are stored
@@ -313,7 +338,7 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
           for (int t = 0; t < NTW; ++t)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
-              v[j][t][mt] = load_dev16(rs, lo + (uint32_t)(s2 * NW * FR + (t * MT + mt) * 256) * 4u);
+              v[j][t][mt] = load_dev16(rs, lo + (uint32_t)(s2 * NWT * FR + (t * MT + mt) * 256) * 4u);
         }
       }
 #pragma unroll
@@ -345,7 +370,7 @@ __global__ __launch_bounds__(256, 1) void splitk_kernel(const char *__restrict__
 #pragma unroll
             for (int i = 0; i < 4; ++i) cur[i] = 4 * q1 + i < NTW ? acc1[4 * q1 + i] : 0.f;
           } else {
-            cur = load_dev16(rs, lo + (uint32_t)(s2 * NW * FR + (NTW * MT + q1) * 256) * 4u);
+            cur = load_dev16(rs, lo + (uint32_t)(s2 * NWT * FR + (NTW * MT + q1) * 256) * 4u);
           }
           tot = s2 == 0 ? cur : tot + cur;
         }
@@ -428,28 +453,30 @@ int device_cus() {
 
 }  // namespace
 
-// Plan: tiles per wave TW and splits S minimising a time model of the
-// busiest CU. Every split of a row block runs on the row block's XCD
-// (workgroup b on XCD b % 8), so the busiest XCD holds ceil(nb / 8) * S
-// units and its busiest CU n = ceil(that / (CUs / 8)) of them, up to `cap`
-// resident at a time (LDS per workgroup). The CU streams at a fixed share of
-// HBM (~28 GB/s) unless its j = min(n, cap) resident units keep too few
-// weight bytes in flight (D stages of weight copies each) to cover the
-// memory latency; its time is n x the unit's bytes (weight rows x kc,
-// activation rows x kc x 2 at about half weight (they come from L2), the
-// fp32 partial sums written and read back when S > 1) over that rate, plus
-// a fixed cost per round of resident units (pipeline fill and drain), plus
-// the combining unit's serial read of the other S - 1 splits' partial sums.
-// The constants are a least-squares fit to 1279 timed plans (every TW x S
-// at 38 shapes, M = 2..64, K = 2048..28672, N = 2048..57344; relative rms
-// error 10 %): over those shapes the model's pick is 1.5 % slower than the
-// fastest plan on average (11 % at worst, the same with each shape left out
-// of the fit), against 29 % (88 %) for the former bytes-per-round model, which
-// counted rounds over all CUs instead of the busiest XCD's (nb = 27, S = 9:
-// 243 units for 256 CUs, but 36 on the 32 CUs of three XCDs) and had no
-// latency bound. Splits whose partial sums exceed kSplitkMaxWorkspace are
-// not considered (at M=32 K=28672 N=32768 a 5-way split of 192-row blocks,
-// 21 MB of partial sums, measured 196.7 us against 171.7 unsplit).
+// Plan: waves per workgroup NW, tiles per wave TW and splits S minimising a
+// time model of the busiest CU. Every split of a row block runs on the row
+// block's XCD (workgroup b on XCD b % 8), so the busiest XCD holds
+// ceil(nb / 8) * S units and its busiest CU n = ceil(that / (CUs / 8)) of
+// them, up to `cap` resident at a time (LDS per workgroup). The CU streams at
+// a fixed share of HBM (~28 GB/s with 4 waves per workgroup, ~36 GB/s with 8,
+// whose waves hide each other's issue and waits) unless its j = min(n, cap)
+// resident units keep too few weight bytes in flight (D stages of weight
+// copies each) to cover the memory latency; its time is n x the unit's bytes
+// (weight rows x kc, activation rows x kc x 2 at about 0.6 weight (they come
+// from L2), the fp32 partial sums written and read back when S > 1) over that
+// rate, plus a fixed cost per round of resident units (pipeline fill and
+// drain: ~1.2 us with 4 waves, ~3.8 us with 8), plus the combining unit's
+// serial read of the other S - 1 splits' partial sums. The constants are a
+// least-squares fit to 2422 timed plans (every NW x TW x S at 38 shapes,
+// M = 2..64, K = 2048..28672, N = 2048..57344; relative rms error 10 %):
+// the model's pick is 0.7 % slower than the fastest plan on average (9 % at
+// worst); the best 4-wave plans
+// alone are 7 % slower on average, and the former bytes-per-round model's
+// picks 29 % (it counted rounds over all CUs instead of the busiest XCD's:
+// nb = 27, S = 9, 243 units for 256 CUs, but 36 on the 32 CUs of three XCDs).
+// Splits whose partial sums exceed kSplitkMaxWorkspace are not considered
+// (at M=32 K=28672 N=32768 a 5-way split of 192-row blocks, 21 MB of partial
+// sums, measured 196.7 us against 171.7 unsplit).
 SplitkPlan splitk_plan(int64_t M, int64_t N, int64_t K, bool gu, bool allow_split) {
   SplitkPlan best{};
   best.ok = false;
@@ -470,63 +497,77 @@ SplitkPlan splitk_plan(int64_t M, int64_t N, int64_t K, bool gu, bool allow_spli
   // Fitted: CU share of HBM (bytes/us), memory latency (us), cost per round
   // (us), activation and partial-sum byte weights, and the combining unit's
   // read of the other splits' partial sums (us per byte).
-  constexpr double kCuRate = 27.81e3, kLatency = 1.112, kRound = 1.167, kActW = 0.508, kPartW = 1.681,
-                   kCombine = 0.03768e-3;
+  constexpr double kCuRate4 = 28.49e3, kCuRate8 = 35.69e3, kLatency = 1.055, kRound4 = 1.236, kRound8 = 3.78,
+                   kActW = 0.592, kPartW = 1.708, kCombine4 = 0.037e-3, kCombine8 = 0.0176e-3;
   double best_t = 0;
-  int force_s = 0, force_tw = 0;
+  int force_s = 0, force_tw = 0, force_nw = 0;
 #ifdef RA_TUNING
   force_s = g_sk_s;
   force_tw = g_sk_tw;
+  force_nw = g_sk_nw;
 #endif
+  for (int nw = 4; nw <= 8; nw += 4)
   for (int tw = 1; tw <= 3; ++tw) {
+    if (force_nw > 0 && nw != force_nw) continue;
     if (force_tw > 0 && tw != force_tw) continue;
     const int ntw = gu ? 2 * tw : tw;
-    const int64_t R = (int64_t)sk::NW * tw * 16;
+    const int64_t R = (int64_t)nw * tw * 16;
     const int64_t nb = (N + R - 1) / R;
     const int smax = (allow_split && nb <= sk::kMaxCounters) ? (int)std::min<int64_t>(stages, 16) : 1;
-    const int d = sk::depth(mt, tw, gu, sk::kMaxD, x1);
-    const int lds = sk::lds_bytes(mt, tw, gu, d, x1) + 4;  // + the flag
+    if (!sk::fits(mt, tw, gu, x1, nw)) continue;
+    const int d = sk::depth(mt, tw, gu, sk::kMaxD, x1, nw);
+    const int lds = sk::lds_bytes(mt, tw, gu, d, x1, nw) + 4;  // + the flag
     const int64_t cap = std::max(kCuLds / ((lds + 511) / 512 * 512), 1);  // resident units per CU
-    const double inflight = (double)d * ntw * 16 * sk::NW * sk::KS;  // weight bytes in flight per unit
+    const double inflight = (double)d * ntw * 16 * nw * sk::KS;  // weight bytes in flight per unit
     for (int S = 1; S <= smax; ++S) {
       if (force_s > 0 && S != force_s) continue;
       const int64_t kst = (stages + S - 1) / S;  // stages per split
       const int64_t se = (stages + kst - 1) / kst;
       if (se != S) continue;                     // a split would be empty
       const int64_t kc = kst * sk::KS;
-      if (S > 1 && sk::kCounterBytes + (size_t)S * nb * sk::part_floats(mt, tw, gu, x1) * 4 > kSplitkMaxWorkspace)
+      if (S > 1 && sk::kCounterBytes + (size_t)S * nb * sk::part_floats(mt, tw, gu, x1, nw) * 4 > kSplitkMaxWorkspace)
         continue;  // partial sums beyond the workspace limit
       const int64_t slots = ((nb + 7) / 8) * 8 * S;  // grid (XCD-grouped row blocks)
       const int64_t n = (((nb + 7) / 8) * S + xcd_cus - 1) / xcd_cus;  // units on the busiest CU
       const int64_t rounds = (n + cap - 1) / cap;
-      const double wbytes = (double)(ntw * 16 * sk::NW) * kc;
+      const double wbytes = (double)(ntw * 16 * nw) * kc;
       const double xbytes = (double)std::min<int64_t>(M, 16 * mt + x1) * kc * 2;
-      const double pbytes = S > 1 ? (double)sk::part_floats(mt, tw, gu, x1) * 4 * (1.0 + 1.0) : 0.0;
-      const double rate = std::min(kCuRate, (double)std::min(n, cap) * inflight / kLatency);
-      const double t = (double)n * (wbytes + kActW * xbytes + kPartW * pbytes) / rate + (double)rounds * kRound +
-                       kCombine * (S - 1) * sk::part_floats(mt, tw, gu, x1) * 4 + 1e-6 * (double)slots;
+      const double pbytes = S > 1 ? (double)sk::part_floats(mt, tw, gu, x1, nw) * 4 * (1.0 + 1.0) : 0.0;
+      const double rate = std::min(nw == 8 ? kCuRate8 : kCuRate4, (double)std::min(n, cap) * inflight / kLatency);
+      const double t = (double)n * (wbytes + kActW * xbytes + kPartW * pbytes) / rate +
+                       (double)rounds * (nw == 8 ? kRound8 : kRound4) +
+                       (nw == 8 ? kCombine8 : kCombine4) * (S - 1) * sk::part_floats(mt, tw, gu, x1, nw) * 4 +
+                       1e-6 * (double)slots;
       if (!best.ok || t < best_t) {
-        best = SplitkPlan{true, mt, tw, S, (int)kc, (int)nb, false, 0, 0, x1};
+        best = SplitkPlan{true, mt, tw, S, (int)kc, (int)nb, false, 0, 0, x1, nw};
         best_t = t;
       }
     }
   }
   if (best.ok && best.S > 1) {
     best.cnt_bytes = sk::kCounterBytes;
-    best.ws_bytes = best.cnt_bytes + (size_t)best.S * best.nb * sk::part_floats(best.mt, best.tw, gu, best.x1) * 4;
+    best.ws_bytes =
+        best.cnt_bytes + (size_t)best.S * best.nb * sk::part_floats(best.mt, best.tw, gu, best.x1, best.nw) * 4;
   }
   return best;
 }
 
 namespace {
 
-template <int DT, int MT, int TW, bool GU, int X1>
+template <int DT, int MT, int TW, bool GU, int X1, int NWT = sk::NW>
 void splitk_go(const SplitkPlan &p, const void *x, int64_t ldx, const int8_t *w, int64_t ldw, const float *scale,
                const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N, int64_t K, void *ws,
                hipStream_t s) {
   const unsigned grid = (unsigned)(p.spread ? (int64_t)p.nb * p.S : ((p.nb + 7) / 8) * 8 * p.S);
   int *cnt = static_cast<int *>(ws);
   float *part = ws ? reinterpret_cast<float *>(static_cast<char *>(ws) + p.cnt_bytes) : nullptr;
+  if (NWT != sk::NW) {  // 8 waves per workgroup
+    hipLaunchKernelGGL((splitk_kernel<DT, MT, TW, GU, X1, sk::kMaxD, NWT>), dim3(grid), dim3(64 * NWT), 0, s,
+                       static_cast<const char *>(x), ldx, reinterpret_cast<const char *>(w), ldw, scale, bias,
+                       bias_dt, static_cast<uint16_t *>(y), ldy, (int)M, (int)N, (int)K, p.kc, p.S, p.nb,
+                       p.spread ? 1 : 0, part, cnt);
+    return;
+  }
 #ifdef RA_TUNING
   if (g_sk_dmax == 2 || g_sk_dmax == 3) {  // forced pipeline depth cap
     auto k = g_sk_dmax == 2 ? splitk_kernel<DT, MT, TW, GU, X1, 2> : splitk_kernel<DT, MT, TW, GU, X1, 3>;
@@ -546,6 +587,16 @@ template <int DT, bool GU>
 void splitk_dispatch(const SplitkPlan &p, const void *x, int64_t ldx, const int8_t *w, int64_t ldw,
                      const float *scale, const void *bias, int bias_dt, void *y, int64_t ldy, int64_t M, int64_t N,
                      int64_t K, void *ws, hipStream_t s) {
+#define RA_SK8(MT_, TW_, X1_)                                                                                    \
+  if constexpr (sk::fits(MT_, TW_, GU, X1_, 8))                                                               \
+    if (p.nw == 8 && p.mt == MT_ && p.tw == TW_ && p.x1 == X1_)                                                \
+      return splitk_go<DT, MT_, TW_, GU, X1_, 8>(p, x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, ws, s);
+  RA_SK8(1, 1, 0) RA_SK8(1, 2, 0) RA_SK8(1, 3, 0)
+  RA_SK8(2, 1, 0) RA_SK8(2, 2, 0) RA_SK8(2, 3, 0)
+  RA_SK8(4, 1, 0) RA_SK8(4, 2, 0) RA_SK8(4, 3, 0)
+  RA_SK8(1, 1, 1) RA_SK8(1, 2, 1) RA_SK8(1, 3, 1)
+  RA_SK8(2, 1, 1) RA_SK8(2, 2, 1) RA_SK8(2, 3, 1)
+#undef RA_SK8
 #define RA_SK(MT_, TW_, X1_)                                                                                     \
   if (p.mt == MT_ && p.tw == TW_ && p.x1 == X1_)                                                               \
     return splitk_go<DT, MT_, TW_, GU, X1_>(p, x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, ws, s);

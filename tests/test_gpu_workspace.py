@@ -11,6 +11,8 @@ split plan), through the C ABI:
   where the split-K plan does not split it runs what a call without a
   workspace runs.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -156,63 +158,68 @@ def test_gateup_splitk_vs_exact_and_oracle(gpu, dt, M, K, inter):
     _check_chain(hr, y64[:, :inter], y64[:, inter:], dt, slack[:, :inter], slack[:, inter:])
 
 
-# One problem per split-K kernel instantiation (GEMM / gate-up, 16*MT-row
-# tiles, the extra row, TW weight tiles per wave), with the plan (TW, S) the
-# time model picks for it, pinned through the workspace size the plan needs.
+# One problem per split-K kernel instantiation the automatic pick reaches
+# (GEMM / gate-up, 16*MT-row tiles, the extra row, TW weight tiles per wave,
+# 4 or 8 waves per workgroup), with the plan (NW, TW, S) the time model picks
+# for it, pinned through the library's planner.
 SPLITK_INSTANCES = [
-    # (gate/up, M, K, N or I, TW, S)
-    (False, 3, 16384, 256, 1, 16), (False, 8, 16384, 4672, 2, 6), (False, 8, 16384, 8256, 3, 5),
-    (False, 17, 16384, 256, 1, 16), (False, 17, 16384, 2624, 2, 10), (False, 17, 16384, 8256, 3, 5),
-    (False, 18, 16384, 256, 1, 16), (False, 18, 16384, 4672, 2, 6), (False, 18, 16384, 8256, 3, 5),
-    (False, 33, 16384, 256, 1, 13), (False, 33, 16384, 3136, 2, 8), (False, 33, 16384, 8256, 3, 5),
-    (False, 34, 16384, 256, 1, 10), (False, 34, 16384, 4160, 2, 6), (False, 34, 16384, 10304, 3, 4),
-    (True, 3, 16384, 256, 1, 16), (True, 5, 16384, 9792, 2, 3), (True, 8, 16384, 8256, 3, 5),
-    (True, 17, 16384, 256, 1, 13), (True, 17, 16384, 5184, 2, 5), (True, 17, 16384, 8256, 3, 5),
-    (True, 18, 16384, 256, 1, 13), (True, 18, 16384, 5184, 2, 5), (True, 18, 20480, 8256, 3, 5),
-    (True, 33, 16384, 256, 1, 10), (True, 33, 16384, 5184, 2, 5), (True, 33, 20480, 8256, 3, 5),
-    (True, 34, 16384, 256, 1, 8), (True, 34, 16384, 5184, 2, 5)]
-# (gate/up with 64-row tiles and three tiles per wave is never planned: its
-# partial sums exceed the 16 MiB workspace limit wherever it would be picked)
+    # (gate/up, M, K, N or I, NW, TW, S)
+    (False, 3, 16384, 128, 4, 1, 16), (False, 5, 32768, 1600, 8, 1, 16), (False, 5, 5120, 20480, 8, 2, 3),
+    (False, 3, 5120, 40960, 8, 3, 2), (False, 17, 16384, 128, 4, 1, 16), (False, 17, 16384, 2624, 8, 1, 10),
+    (False, 17, 16384, 10304, 8, 2, 5), (False, 17, 24576, 10304, 8, 3, 8), (False, 24, 5120, 128, 4, 1, 8),
+    (False, 18, 11008, 3136, 8, 1, 8), (False, 17, 5120, 20480, 8, 2, 3), (False, 32, 5120, 10816, 4, 3, 4),
+    (False, 17, 5120, 40960, 8, 3, 2), (False, 33, 16384, 128, 4, 1, 13), (False, 33, 24576, 1600, 8, 1, 16),
+    (False, 33, 16384, 10304, 8, 2, 5), (False, 33, 32768, 10304, 8, 3, 8), (False, 33, 4096, 128, 4, 1, 4),
+    (False, 33, 11008, 3136, 8, 1, 8), (False, 33, 14336, 10304, 8, 2, 5), (False, 33, 8192, 40960, 4, 3, 1),
+    (True, 3, 8192, 128, 4, 1, 11), (True, 8, 16384, 3136, 8, 1, 8), (True, 3, 16384, 10816, 8, 2, 5),
+    (True, 17, 16384, 128, 4, 1, 13), (True, 17, 16384, 3136, 8, 1, 8), (True, 17, 16384, 10304, 8, 2, 5),
+    (True, 17, 8192, 128, 4, 1, 8), (True, 24, 16384, 3136, 8, 1, 8), (True, 18, 16384, 10304, 8, 2, 5),
+    (True, 18, 16384, 40960, 4, 3, 1), (True, 33, 16384, 128, 4, 1, 10), (True, 33, 16384, 3136, 8, 1, 8),
+    (True, 33, 16384, 10304, 8, 2, 5), (True, 33, 16384, 11584, 4, 3, 4), (True, 48, 4096, 128, 4, 1, 4),
+    (True, 33, 4096, 8256, 8, 1, 3), (True, 33, 4096, 40960, 4, 3, 1)]
 
 
-def _splitk_ws_bytes(gu, M, K, N, tw, S):
-    """Workspace of split-K plan (tw, S): the counter block, then S fp32
-    partial-sum blocks per row block of 64*tw output columns (4 waves of
-    NTW*MT fragments of 256 floats, plus one group for the extra row)."""
-    x1 = 1 if M in (17, 33) else 0
-    mt = M // 16 if x1 else (1 if M <= 16 else (2 if M <= 32 else 4))
-    ntw = 2 * tw if gu else tw
-    part = 4 * (ntw * mt + x1 * ((ntw + 3) // 4)) * 256
-    return _backend.WORKSPACE_COUNTER_BYTES + S * (-(-N // (64 * tw))) * part * 4
+class _SplitkPlan(ctypes.Structure):
+    """ra::SplitkPlan (rotalabs-accel_amd/csrc/ra_internal.h)."""
+    _fields_ = [("ok", ctypes.c_bool), ("mt", ctypes.c_int), ("tw", ctypes.c_int), ("S", ctypes.c_int),
+                ("kc", ctypes.c_int), ("nb", ctypes.c_int), ("spread", ctypes.c_bool),
+                ("cnt_bytes", ctypes.c_size_t), ("ws_bytes", ctypes.c_size_t), ("x1", ctypes.c_int),
+                ("nw", ctypes.c_int)]
+
+
+def _splitk_plan(M, N, K, gu):
+    """The library's split-K plan (its C++ planner, exported from the shared
+    library under its mangled name)."""
+    f = getattr(_backend.load(), "_ZN2ra11splitk_planElllbb")
+    f.restype = _SplitkPlan
+    f.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_bool, ctypes.c_bool]
+    return f(M, N, K, gu, True)
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("gu,M,K,N,tw,S", SPLITK_INSTANCES)
-def test_splitk_every_instantiation_exact(gpu, dt, gu, M, K, N, tw, S):
-    """Exact known answers from every split-K instantiation the library
-    dispatches (both dtypes, GEMM and gate/up): x in {-1, 0, 1} with at most
-    ~200 non-zeros per row and q in [-lim, lim] keep every sum an integer
-    below 2^11, exact in fp32 whatever the order, so any tile, extra-row,
-    split or combine mistake is a mismatch. The inputs are generated and the
-    exact sums formed on the GPU (fp32 products of small integers)."""
+@pytest.mark.parametrize("gu,M,K,N,nw,tw,S", SPLITK_INSTANCES)
+def test_splitk_every_instantiation_exact(gpu, dt, gu, M, K, N, nw, tw, S):
+    """Exact known answers from every split-K instantiation the automatic pick
+    reaches (both dtypes, GEMM and gate/up): x in {-1, 0, 1} with ~120
+    non-zeros per row and q in [-lim, lim] keep every sum an integer below
+    2^11, exact in fp32 whatever the order, so any tile, extra-row, split or
+    combine mistake is a mismatch. The inputs are generated and the exact sums
+    formed on the GPU (fp32 products of small integers)."""
     lib = _backend.load()
     dcode = _backend.dtype_code(dt)
-    size = lib.ra_w8a16_gateup_workspace_size(M, N, K, dcode) if gu else \
-        lib.ra_w8a16_gemm_workspace_size(M, N, K, dcode)
-    want = _splitk_ws_bytes(gu, M, K, N, tw, S)
-    # (from M = 33 over 8192+ rows the reported size also covers the 64-row
-    # tiles' split plan, which can need more)
-    assert size == want or (not gu and M > 32 and N >= 8192 and size > want), "the plan is not (TW, S)"
-    print(f"  split-K instance gu={gu} M={M} K={K} N={N} tw={tw} S={S} {dt}", flush=True)
+    p = _splitk_plan(M, N, K, gu)
+    assert p.ok and (p.nw, p.tw, p.S) == (nw, tw, S), f"the plan is ({p.nw}, {p.tw}, {p.S})"
+    print(f"  split-K instance gu={gu} M={M} K={K} N={N} nw={nw} tw={tw} S={S} {dt}", flush=True)
     g = torch.Generator(device=gpu).manual_seed(M * 3 + K + N)
     lim = 3 if dt == torch.float16 else 1
     rows = 2 * N if gu else N
     x = torch.randint(-1, 2, (M, K), device=gpu, generator=g).float()
-    x = x * (torch.rand(M, K, device=gpu, generator=g) < 200.0 / K)
+    x = x * (torch.rand(M, K, device=gpu, generator=g) < 120.0 / K)
     q = torch.randint(-lim, lim + 1, (rows, K), device=gpu, generator=g, dtype=torch.int8)
     s = torch.full((rows,), 2.0 ** -4, device=gpu)
     sums = ((x @ q.float().T) * 2.0 ** -4).double().cpu()
     if gu:
+        assert lib.ra_w8a16_gateup_workspace_size(M, N, K, dcode) == (p.ws_bytes if S > 1 else 0)
         h = ra.int8_gateup_swiglu(x.to(dt), q, s)
         torch.cuda.synchronize()
         zero = torch.zeros(M, N, dtype=torch.float64)
