@@ -93,35 +93,39 @@ bool short_k_batch(const GemmArgs &a) {
          (a.M <= 48 && a.K <= 1024 && a.N <= 12288);
 }
 
-// Where the split-K kernel is measured ahead (same run, bf16, us, graph
-// replay of cold weights; the other kernel -> split K):
+// Where the split-K kernel (4- or 8-wave plans) is measured ahead (same run,
+// bf16, us, graph replay of cold weights; the other kernel -> split K):
 //  * M = 2..32: K >= 16384 (M=16 K=28672 N=28672 197.0 -> 148.7, M=32
-//    N=14336 131.0 -> 83.1, M=8 K=16384 N=28672 90.4 -> 81.1; M = 2..4 level
-//    within 4 %); from K = 5120 over 14336+ weight rows (M=16 K=5120
-//    N=28672 43.4 -> 29.6, M=2 K=11008 N=28672 62.0 -> 55.4; at N = 57344
-//    with K = 8192 / 14336 and M <= 8 the small-batch kernel stays 2-4 %
-//    ahead); M >= 16 from K = 11008 (M=16 K=11008 N=8192 22.2 -> 20.0);
-//    M >= 24 over at most 4096 rows (M=24 K=8192 N=4096 16.4 -> 14.5);
-//    M = 32 (K=5120 N=8192 16.4 -> 16.0, K=8192 N=8192 22.1 -> 21.2). The
-//    small-batch kernel stays ahead below those (M=8 K=8192 N=8192 15.3
-//    against 16.8, M=24 K=8192 N=8192 18.9 against 21.9).
-//  * M = 33..64 against the 64-row tiles: K >= 14336 (M=33 K=16384 N=16384
-//    74.7 -> 58.4, M=64 K=16384 N=32768 146.7 -> 128.0) except M > 56 over
-//    8192..16384 rows (M=64 K=28672 N=8192 60.5 against 66.2); up to M = 56
-//    K >= 8192 over 32768+ rows (M=33 K=8192 N=32768 73.5 -> 67.5; at M=64
-//    N=57344 the tiles stay ahead, 122.4 against 133.8); at most 4096 rows from
-//    K = 4096, against the small-batch kernel (M=64 K=8192 N=4096 32.8 ->
-//    20.2, M=64 K=4096 N=4096 18.4 -> 14.9).
+//    N=14336 131.0 -> 83.1); from K = 5120 over 14336+ weight rows (M=16
+//    K=5120 N=28672 43.3 -> 27.4, M=2 K=11008 N=28672 61.5 -> 53.8); from
+//    K = 11008 (M=8 K=14336 N=4096 16.0 -> 14.7, M=4 K=11008 N=8192 19.6 ->
+//    18.7; M = 2..4 at K=14336 N=8192 2 % behind); M >= 16 from K = 8192
+//    (M=16 K=8192 N=4096 12.6 -> 11.5, N=8192 17.1 -> 16.4); M >= 24 from
+//    K = 5120 (M=24 K=5120 N=8192 14.6 -> 14.2, K=8192 N=8192 19.0 -> 17.5).
+//    The small-batch kernel stays ahead below those (M=8 K=8192 N=8192 15.4
+//    against 15.8, M=16 K=5120 N=8192 12.4 against 13.5).
+//  * M = 33..64 against the 64-row tiles: up to M = 48 from K = 8192 (M=33
+//    K=8192 N=8192 25.5 -> 22.7, N=16384 41.2 -> 33.0); over 32768+ rows
+//    from K = 4096 (M=40 K=4096 N=32768 39.6 -> 33.1, M=64 K=8192 66.5 ->
+//    62.5); from K = 14336 except M > 56 over at most 8192 rows, where the
+//    two are level (M=64 K=16384 N=16384 67.9 -> 63.9; M=64 K=16384 N=8192
+//    38.8 against 39.9); at most 4096 rows from K = 4096, against the
+//    small-batch kernel (M=64 K=8192 N=4096 32.8 -> 19.8, M=64 K=4096 N=4096
+//    18.4 -> 14.8). The tiles stay ahead at K = 4096 over 8192-16384 rows
+//    (M=64 N=8192 15.1 against 18.7) and at M=64 K=8192 N=8192 (23.7 against
+//    24.4).
 bool splitk_wanted(const GemmArgs &a) {
   if (a.M < 2 || a.M > kSkinnyMaxM) return false;
   if (a.M <= 32) {
     if (a.K >= kSplitkMinK) return true;
     if (a.K < 5120) return false;
-    return a.N >= 14336 || (a.M >= 16 && a.K >= 11008) || (a.M >= 24 && a.N <= 4096) || a.M >= 32;
+    return a.N >= 14336 || a.K >= 11008 || (a.M >= 16 && a.K >= 8192) || a.M >= 24;
   }
   if (a.N <= 4096) return a.K >= 4096;
-  if (a.K >= 14336) return !(a.M > 56 && a.N >= 8192 && a.N <= 16384);
-  return a.M <= 56 && a.K >= 8192 && a.N >= 32768;
+  if (a.M <= 48 && a.K >= 8192) return true;
+  if (a.N >= 32768) return a.K >= 4096;
+  if (a.K >= 14336) return a.N > 8192 || a.M <= 56;
+  return false;
 }
 
 // The split-K kernel runs where it is wanted and its plan either does not
@@ -137,16 +141,23 @@ bool splitk_selected(const GemmArgs &a, bool have_ws) {
 // us, the one-pass gate/up kernels -> split K): K >= 16384; M = 33..64,
 // where the one-pass kernels take two passes over the rows (M=33 K=8192
 // I=28672 169.1 -> 109.2, M=64 235.9 -> 115.9, M=40 K=4096 I=14336 60.8 ->
-// 34.0, M=64 K=3584 I=18944 83.2 -> 59.5), except below M = 48 over at most
-// 4096 gate rows at K < 8192 (M=33 K=4096 I=1792 14.9 against 16.7); from
-// K = 8192 over at most 4096 gate rows, where the one-pass kernels leave CUs
-// idle (M=2 K=8192 I=3584 29.3 -> 16.1, M=32 K=12288 I=4096 71.2 -> 25.5).
-// Below that the one-pass kernels stay ahead (M=17 K=8192 I=28672 79.2
-// against 90.5, M=2 K=4096 I=11008 18.0 against 24.7).
+// 34.0), except below M = 48 over at most 4096 gate rows at K < 8192 (M=33
+// K=4096 I=1792 14.9 against 16.7); from K = 8192 over at most 4096 gate
+// rows, where the one-pass kernels leave CUs idle (M=2 K=8192 I=3584 29.3 ->
+// 16.1, M=32 K=12288 I=4096 71.2 -> 25.5); with 8-wave plans also from
+// M = 24 (M=32 K=4096 I=14336 31.7 -> 27.2, M=24 K=5120 I=13824 35.3 ->
+// 31.2), from 16 rows at K = 8192 (M=17 K=8192 I=28672 79.0 -> 73.1, M=32
+// I=14336 53.6 -> 42.9) and where K is not a multiple of 1024, so the
+// one-pass kernels' K chunks are 512 (M=16 K=3584 I=18944 35.2 -> 29.5).
+// The one-pass kernels stay ahead below M = 24 at K = 4096 (M=2 K=4096
+// I=11008 18.2 against 24.7; M=17 I=14336 26.3 against 28.7), level at
+// K=5120 I=13824, and ahead below 16 rows at K = 8192 (M=2 K=8192 I=14336
+// 38.1 against 40.5).
 bool gateup_splitk_wanted(int64_t M, int64_t I, int64_t K) {
   if (M < 2 || M > kSkinnyMaxM) return false;
   if (K >= kSplitkMinK || (K >= 8192 && I <= 4096)) return true;
-  return M > 32 && (I > 4096 || M >= 48);
+  if (M > 32) return I > 4096 || M >= 48;
+  return M >= 24 || (M >= 16 && K >= 8192) || K % 1024 != 0;
 }
 
 int select_variant(const GemmArgs &a, bool have_ws) {

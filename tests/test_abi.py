@@ -91,9 +91,9 @@ def test_variant_selection_fallbacks():
     assert lib.ra_w8a16_gemm_select(3, 8192, 8192, 1) == 6   # M = 3..64, K % 128 == 0: small-batch kernel
     assert lib.ra_w8a16_gemm_select(17, 8192, 28672, 1) == 7  # ... with K >= 16384: split K over workgroups
     assert lib.ra_w8a16_gemm_select(16, 4096, 11008, 1) == 7  # ... from 16 rows, K >= 11008 over N <= 4096
-    assert lib.ra_w8a16_gemm_select(15, 4096, 11008, 1) == 6
-    assert lib.ra_w8a16_gemm_select(16, 4097, 11008, 1) == 7  # ... and over more rows from K = 11008
-    assert lib.ra_w8a16_gemm_select(16, 8192, 8192, 1) == 6   # below that the small-batch kernel
+    assert lib.ra_w8a16_gemm_select(15, 4096, 11008, 1) == 7  # ... at any M from K = 11008
+    assert lib.ra_w8a16_gemm_select(16, 8192, 8192, 1) == 7   # ... from 16 rows at K = 8192
+    assert lib.ra_w8a16_gemm_select(15, 8192, 8192, 1) == 6   # below that the small-batch kernel
     assert lib.ra_w8a16_gemm_select(64, 8192, 28672, 1) == 2  # M = 33..64, N >= 8192: 64-row tiles
     assert lib.ra_w8a16_gemm_select(4, 8192, 1040, 1) == 1   # K % 128 != 0: split-K MFMA kernel
     assert lib.ra_w8a16_gemm_select(1, 64, 50, 0) == 3     # K % 16 != 0 -> generic
@@ -111,15 +111,17 @@ def test_variant_selection_fallbacks():
     # M = 17..32, K = 2048..4096 over 28672+ rows: the split-K kernel without a split (no workspace)
     (32, 28672, 4096, 7), (17, 28672, 4096, 7), (20, 40960, 2048, 7), (24, 24576, 4096, 6),
     (16, 28672, 4096, 6),
-    # M = 2..32 from K = 5120: split K over 14336+ rows, from 16 rows at K >= 11008, from 24 rows
-    # over at most 4096 rows, at 32 rows; the small-batch kernel below that
+    # M = 2..32 from K = 5120: split K over 14336+ rows, at any M from K = 11008, from 16 rows at
+    # K = 8192, from 24 rows; the small-batch kernel below that
     (32, 27648, 5120, 7), (2, 28672, 5120, 7), (8, 14336, 8192, 7), (16, 8192, 11008, 7),
-    (24, 4096, 8192, 7), (32, 8192, 5120, 7), (8, 8192, 8192, 6), (24, 8192, 8192, 6), (2, 4096, 14336, 6),
-    # M = 33..64: split K from K = 14336 (not at M > 56 over 8192..16384 rows), from K = 8192 over
-    # 32768+ rows, over at most 4096 rows from K = 4096; else the 64-row tiles
+    (24, 4096, 8192, 7), (32, 8192, 5120, 7), (24, 8192, 5120, 7), (2, 4096, 14336, 7), (16, 4096, 8192, 7),
+    (8, 8192, 8192, 6), (16, 8192, 5120, 6), (4, 4096, 8192, 6),
+    # M = 33..64: split K up to 48 rows from K = 8192, over 32768+ rows from K = 4096, from
+    # K = 14336 (not at M > 56 over 8192 rows), over at most 4096 rows from K = 4096; else the
+    # 64-row tiles
     (33, 16384, 16384, 7), (48, 8192, 28672, 7), (64, 32768, 16384, 7), (40, 32768, 8192, 7),
-    (64, 4096, 8192, 7), (64, 16384, 16384, 2), (64, 8192, 28672, 2), (40, 16384, 8192, 2),
-    (48, 16384, 4096, 2)])
+    (64, 4096, 8192, 7), (64, 16384, 16384, 7), (40, 16384, 8192, 7), (48, 32768, 4096, 7),
+    (64, 8192, 28672, 2), (48, 16384, 4096, 2), (64, 8192, 8192, 2), (56, 8192, 8192, 2)])
 def test_variant_selection_short_k_and_wide(M, N, K, expect):
     lib = _backend.load()
     assert lib.ra_w8a16_gemm_select(M, N, K, 1) == expect
@@ -217,13 +219,18 @@ def test_select_agrees_with_the_workspace_size():
 
 
 def test_gateup_workspace_only_where_gateup_splits():
-    """The gate/up product runs the split-K kernel from K = 16384, at M = 33..64,
-    and from K = 8192 over at most 4096 gate rows; elsewhere the size is 0, so
-    the Python layer allocates no workspace it never uses."""
+    """The gate/up product runs the split-K kernel from K = 16384, from K = 8192
+    over at most 4096 gate rows, at M = 33..64, and at M = 2..32 from 24 rows,
+    from 16 rows at K = 8192 or where K is not a multiple of 1024; elsewhere
+    the size is 0,
+    so the Python layer allocates no workspace it never uses. A plan that does
+    not split K needs none either."""
     lib = _backend.load()
-    assert lib.ra_w8a16_gateup_workspace_size(17, 28672, 8192, 1) == 0     # the one-pass kernels
-    assert lib.ra_w8a16_gateup_workspace_size(32, 14336, 4096, 1) == 0
+    assert lib.ra_w8a16_gateup_workspace_size(16, 14336, 4096, 1) == 0     # the one-pass kernels
+    assert lib.ra_w8a16_gateup_workspace_size(17, 28672, 8192, 1) == 0     # a one-split plan
+    assert lib.ra_w8a16_gateup_workspace_size(32, 14336, 4096, 1) > _backend.WORKSPACE_COUNTER_BYTES
     assert lib.ra_w8a16_gateup_workspace_size(8, 4097, 8192, 1) == 0
+    assert lib.ra_w8a16_gateup_workspace_size(16, 4097, 8192, 1) > _backend.WORKSPACE_COUNTER_BYTES
     assert lib.ra_w8a16_gateup_workspace_size(17, 3000, 16384, 1) > _backend.WORKSPACE_COUNTER_BYTES
     assert lib.ra_w8a16_gateup_workspace_size(1, 3000, 16384, 1) == 0      # the row GEMV
     assert lib.ra_w8a16_gateup_workspace_size(48, 3000, 4096, 1) > _backend.WORKSPACE_COUNTER_BYTES

@@ -113,10 +113,14 @@ def _check_chain(h, g64, u64, dt, gslack, uslack):
                                         # below K = 16384: M = 33..64 (from 48 rows or over 4096+ gate rows),
                                         # and at most 4096 gate rows from K = 8192
                                         (48, 4096, 3000), (33, 3584, 4200), (64, 8192, 2000), (2, 8192, 3584),
-                                        (24, 12288, 1000)])
+                                        (24, 12288, 1000),
+                                        # M = 2..32: from 24 rows, from 16 rows at K = 8192, K not a
+                                        # multiple of 1024
+                                        (24, 4096, 6000), (16, 8192, 5000), (8, 4224, 3000)])
 def test_gateup_splitk_vs_exact_and_oracle(gpu, dt, M, K, inter):
     """The gate/up + SwiGLU GEMM through the split-K kernel (K >= 16384, M =
-    33..64, or at most 4096 gate rows from K = 8192; a workspace is asked for
+    33..64, at most 4096 gate rows from K = 8192, or M = 2..32 from 24 rows,
+    from 16 rows at K = 8192 or with K not a multiple of 1024; a workspace is asked for
     and given). Exact integer sums make the fp32 gate
     and up values order-independent, so the output must be the reference
     composition's roundings of them bit for bit (up to silu's own fp32
