@@ -435,12 +435,21 @@ bool sk_shape_ok(int x_dt, const void *x, int64_t ldx, const int8_t *w, int64_t 
   return true;
 }
 
-bool x1_allowed() {
+// The extra-row form (M = 17 or 33: one 16-row MFMA tile fewer, the last row
+// on the VALU), where it is measured ahead (same run, bf16, us, split-K
+// kernel with the padded tile -> extra row): at M = 33 (M=33 K=4096 N=28672
+// 31.0 -> 27.1, K=8192 N=8192 22.8 -> 21.1, gate/up K=8192 I=28672 92.6 ->
+// 82.3), for the gate/up product at M = 17 (K=8192 I=28672 75.2 -> 73.5,
+// K=4096 I=11008 28.1 -> 22.2) and for the GEMM at M = 17 from K = 16384
+// (K=28672 N=8192 49.5 -> 45.6); the GEMM at M = 17 below K = 16384 is level
+// over many rows and behind over few (K=4096 N=6144 11.4 against 13.0,
+// K=11008 N=4096 15.5 against 16.1).
+bool x1_wanted(int64_t M, int64_t K, bool gu) {
 #ifdef RA_TUNING
-  return g_sk_x1 == 0;  // tuning builds: 1 turns the extra-row form off
-#else
-  return true;
+  if (g_sk_x1 == 1) return false;  // tuning builds: 1 turns the extra-row form off, 2 on at any K
+  if (g_sk_x1 == 2) return M == 17 || M == 33;
 #endif
+  return M == 33 || (M == 17 && (gu || K >= 16384));
 }
 
 int device_cus() {
@@ -482,11 +491,7 @@ SplitkPlan splitk_plan(int64_t M, int64_t N, int64_t K, bool gu, bool allow_spli
   best.ok = false;
   if (M < 1 || M > sk::kMaxM || K < sk::KS || K % sk::KS != 0 || N < 1) return best;
   int mt = sk_mt(M), x1 = 0;
-  // M = 17 or 33 at K >= 16384: one 16-row MFMA tile fewer, the last row on
-  // the VALU (same-run A/B, us, padded tile -> extra row: M=17 K=28672
-  // N=8192 bf16 49.5 -> 45.6, M=33 K=16384 N=4096 25.3 -> 23.8, M=17 K=16384
-  // N=16384 level; at M=17 K=11008 N=4096 16.3 -> 17.0, so not below 16384)
-  if ((M == 17 || M == 33) && K >= 16384 && x1_allowed()) {
+  if (x1_wanted(M, K, gu)) {
     mt = (int)(M / 16);
     x1 = 1;
   }

@@ -173,14 +173,21 @@ SPLITK_INSTANCES = [
     (False, 17, 16384, 10304, 8, 2, 5), (False, 17, 24576, 10304, 8, 3, 8), (False, 24, 5120, 128, 4, 1, 8),
     (False, 18, 11008, 3136, 8, 1, 8), (False, 17, 5120, 20480, 8, 2, 3), (False, 32, 5120, 10816, 4, 3, 4),
     (False, 17, 5120, 40960, 8, 3, 2), (False, 33, 16384, 128, 4, 1, 13), (False, 33, 24576, 1600, 8, 1, 16),
-    (False, 33, 16384, 10304, 8, 2, 5), (False, 33, 32768, 10304, 8, 3, 8), (False, 33, 4096, 128, 4, 1, 4),
-    (False, 33, 11008, 3136, 8, 1, 8), (False, 33, 14336, 10304, 8, 2, 5), (False, 33, 8192, 40960, 4, 3, 1),
+    (False, 33, 16384, 10304, 8, 2, 5), (False, 33, 32768, 10304, 8, 3, 8), (False, 33, 4096, 128, 4, 1, 8),
+    (False, 33, 11008, 3136, 8, 1, 8), (False, 33, 14336, 10304, 8, 2, 5), (False, 33, 8192, 40960, 8, 3, 2),
+    (False, 16, 9088, 10944, 4, 3, 4), (False, 24, 2048, 29568, 4, 2, 1), (False, 33, 4096, 33344, 4, 3, 1),
+    (False, 34, 4608, 64, 4, 1, 6), (False, 63, 6784, 3328, 8, 1, 8), (False, 48, 8832, 10496, 8, 2, 5),
+    (False, 38, 8192, 21888, 4, 3, 2),
     (True, 3, 8192, 128, 4, 1, 11), (True, 8, 16384, 3136, 8, 1, 8), (True, 3, 16384, 10816, 8, 2, 5),
     (True, 17, 16384, 128, 4, 1, 13), (True, 17, 16384, 3136, 8, 1, 8), (True, 17, 16384, 10304, 8, 2, 5),
     (True, 17, 8192, 128, 4, 1, 8), (True, 24, 16384, 3136, 8, 1, 8), (True, 18, 16384, 10304, 8, 2, 5),
     (True, 18, 16384, 40960, 4, 3, 1), (True, 33, 16384, 128, 4, 1, 10), (True, 33, 16384, 3136, 8, 1, 8),
     (True, 33, 16384, 10304, 8, 2, 5), (True, 33, 16384, 11584, 4, 3, 4), (True, 48, 4096, 128, 4, 1, 4),
-    (True, 33, 4096, 8256, 8, 1, 3), (True, 33, 4096, 40960, 4, 3, 1)]
+    (True, 33, 4096, 8256, 8, 1, 3), (True, 33, 4096, 40960, 4, 3, 1),
+    (True, 3, 128, 16576, 4, 2, 1), (True, 13, 2304, 20928, 4, 3, 2), (True, 17, 128, 34688, 4, 3, 1),
+    (True, 17, 128, 17216, 4, 2, 1), (True, 23, 1536, 64, 4, 1, 4), (True, 28, 128, 16576, 4, 2, 1),
+    (True, 33, 128, 17856, 4, 2, 1), (True, 64, 3200, 8320, 8, 1, 3), (True, 40, 128, 17216, 4, 2, 1),
+    (True, 60, 128, 32896, 4, 3, 1)]
 
 
 class _SplitkPlan(ctypes.Structure):
