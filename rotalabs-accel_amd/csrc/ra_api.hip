@@ -103,7 +103,16 @@ bool short_k_batch(const GemmArgs &a) {
 //    (M=16 K=8192 N=4096 12.6 -> 11.5, N=8192 17.1 -> 16.4); M >= 24 from
 //    K = 5120 (M=24 K=5120 N=8192 14.6 -> 14.2, K=8192 N=8192 19.0 -> 17.5).
 //    The small-batch kernel stays ahead below those (M=8 K=8192 N=8192 15.4
-//    against 15.8, M=16 K=5120 N=8192 12.4 against 13.5).
+//    against 15.8, M=16 K=5120 N=8192 12.4 against 13.5), except from 28
+//    rows at K = 3072..4096 over at most 4096 rows, where it has too few
+//    workgroups (M=32 K=4096 N=2048 11.2 -> 9.6, K=3072 N=1024 9.6 -> 8.9;
+//    M=24 K=3072 level, K=4096 N=4096 10.0 against 10.5).
+//  * M = 33 (one 16-row tile fewer, the extra row on the VALU): over 28672+
+//    rows (M=33 K=3072 N=28672 28.1 -> 21.4, K=1024 N=57344 28.7 -> 19.3),
+//    over 11008+ rows from K = 4096 (K=4096 N=11008 20.4 -> 18.4), over
+//    6144+ rows from K = 5120 (K=5120 N=6144 19.7 -> 15.5); the 64-row tiles
+//    and the small-batch kernel stay ahead below those (K=4096 N=8192 16.1
+//    against 17.5, K=2048 N=8192 9.9 against 11.3).
 //  * M = 33..64 against the 64-row tiles: up to M = 48 from K = 8192 (M=33
 //    K=8192 N=8192 25.5 -> 22.7, N=16384 41.2 -> 33.0); over 32768+ rows
 //    from K = 4096 (M=40 K=4096 N=32768 39.6 -> 33.1, M=64 K=8192 66.5 ->
@@ -118,9 +127,11 @@ bool splitk_wanted(const GemmArgs &a) {
   if (a.M < 2 || a.M > kSkinnyMaxM) return false;
   if (a.M <= 32) {
     if (a.K >= kSplitkMinK) return true;
+    if (a.M >= 28 && a.K >= 3072 && a.N <= 4096) return true;
     if (a.K < 5120) return false;
     return a.N >= 14336 || a.K >= 11008 || (a.M >= 16 && a.K >= 8192) || a.M >= 24;
   }
+  if (a.M == 33 && (a.N >= 28672 || (a.K >= 4096 && a.N >= 11008) || (a.K >= 5120 && a.N >= 6144))) return true;
   if (a.N <= 4096) return a.K >= 4096;
   if (a.M <= 48 && a.K >= 8192) return true;
   if (a.N >= 32768) return a.K >= 4096;
@@ -152,11 +163,19 @@ bool splitk_selected(const GemmArgs &a, bool have_ws) {
 // The one-pass kernels stay ahead below M = 24 at K = 4096 (M=2 K=4096
 // I=11008 18.2 against 24.7; M=17 I=14336 26.3 against 28.7), level at
 // K=5120 I=13824, and ahead below 16 rows at K = 8192 (M=2 K=8192 I=14336
-// 38.1 against 40.5).
+// 38.1 against 40.5). Over few gate rows the one-pass kernels have too few
+// workgroups: split K from K = 2048 over at most 4096 gate rows and from
+// K = 3072 over at most 8192 (M=8 K=4096 I=2048 16.8 -> 9.4, M=16 K=6144
+// I=4096 27.1 -> 13.6, M=2 K=3072 I=8192 14.1 -> 13.4; at K = 1024 the
+// one-pass kernels stay ahead, M=2 I=4096 6.8 against 7.9). At M = 17 the
+// extra-row form makes split K the faster at any K and I (K=4096 I=4096
+// 22.3 -> 12.8, K=4096 I=11008 23.7 -> 22.2, K=2048 I=28672 26.9 -> 22.6;
+// at most 4 % behind at K=2048-6144 I=11008).
 bool gateup_splitk_wanted(int64_t M, int64_t I, int64_t K) {
   if (M < 2 || M > kSkinnyMaxM) return false;
   if (K >= kSplitkMinK || (K >= 8192 && I <= 4096)) return true;
   if (M > 32) return I > 4096 || M >= 48;
+  if (M == 17 || (K >= 2048 && I <= 4096) || (K >= 3072 && I <= 8192)) return true;
   return M >= 24 || (M >= 16 && K >= 8192) || K % 1024 != 0;
 }
 

@@ -80,7 +80,8 @@ def test_argument_checks_without_device_work():
     assert lib.ra_w8a16_gemm_noalloc(n, 0, 0, n, 0, n, n, 0, n, 0, 0, 4, 4, n) == 0
 
 
-@pytest.mark.parametrize("M,expect", [(1, 5), (2, 6), (3, 6), (4, 6), (5, 6), (16, 6), (32, 6), (33, 2), (64, 2), (65, 2), (2048, 2)])
+@pytest.mark.parametrize("M,expect", [(1, 5), (2, 6), (3, 6), (4, 6), (5, 6), (16, 6), (32, 6), (33, 7), (34, 2), (64, 2), (65, 2),
+                                      (2048, 2)])
 def test_variant_selection(M, expect):
     assert _backend.load().ra_w8a16_gemm_select(M, 11008, 4096, 0) == expect
 
@@ -107,7 +108,7 @@ def test_variant_selection_fallbacks():
     (1, 11008, 4096, 5),
     # M = 33..56 at short K over at most ~12K rows: the small-batch kernel instead of the 64-row tiles
     (33, 8192, 2048, 6), (40, 12288, 3072, 6), (48, 11008, 1024, 6), (56, 8192, 2048, 6),
-    (48, 9216, 2048, 2), (33, 13824, 2048, 2), (64, 8192, 2048, 2), (33, 11008, 4096, 2),
+    (48, 9216, 2048, 2), (33, 13824, 2048, 2), (64, 8192, 2048, 2), (40, 11008, 4096, 2),
     # M = 17..32, K = 2048..4096 over 28672+ rows: the split-K kernel without a split (no workspace)
     (32, 28672, 4096, 7), (17, 28672, 4096, 7), (20, 40960, 2048, 7), (24, 24576, 4096, 6),
     (16, 28672, 4096, 6),
@@ -116,6 +117,12 @@ def test_variant_selection_fallbacks():
     (32, 27648, 5120, 7), (2, 28672, 5120, 7), (8, 14336, 8192, 7), (16, 8192, 11008, 7),
     (24, 4096, 8192, 7), (32, 8192, 5120, 7), (24, 8192, 5120, 7), (2, 4096, 14336, 7), (16, 4096, 8192, 7),
     (8, 8192, 8192, 6), (16, 8192, 5120, 6), (4, 4096, 8192, 6),
+    # ... and from 28 rows at K = 3072..4096 over at most 4096 rows
+    (32, 2048, 4096, 7), (28, 4096, 3072, 7), (24, 2048, 4096, 6), (32, 6144, 4096, 6), (32, 4096, 2048, 6),
+    # M = 33 (the extra-row form): over 28672+ rows, over 11008+ from K = 4096, over 6144+ from
+    # K = 5120; the tiles or the small-batch kernel below
+    (33, 28672, 3072, 7), (33, 57344, 1024, 7), (33, 11008, 4096, 7), (33, 6144, 5120, 7),
+    (33, 8192, 4096, 2), (33, 16384, 2048, 2), (33, 4096, 3072, 6),
     # M = 33..64: split K up to 48 rows from K = 8192, over 32768+ rows from K = 4096, from
     # K = 14336 (not at M > 56 over 8192 rows), over at most 4096 rows from K = 4096; else the
     # 64-row tiles
@@ -125,7 +132,7 @@ def test_variant_selection_fallbacks():
 def test_variant_selection_short_k_and_wide(M, N, K, expect):
     lib = _backend.load()
     assert lib.ra_w8a16_gemm_select(M, N, K, 1) == expect
-    if expect == 7 and K <= 4096:   # the unsplit split-K kernel needs no workspace
+    if expect == 7 and K <= 4096 and M <= 32 and N >= 28672:   # the unsplit split-K kernel: no workspace
         assert lib.ra_w8a16_gemm_workspace_size(M, N, K, 1) == 0
 
 
@@ -220,17 +227,20 @@ def test_select_agrees_with_the_workspace_size():
 
 def test_gateup_workspace_only_where_gateup_splits():
     """The gate/up product runs the split-K kernel from K = 16384, from K = 8192
-    over at most 4096 gate rows, at M = 33..64, and at M = 2..32 from 24 rows,
-    from 16 rows at K = 8192 or where K is not a multiple of 1024; elsewhere
-    the size is 0,
+    over at most 4096 gate rows, at M = 33..64, and at M = 2..32 at M = 17,
+    from 24 rows, from 16 rows at K = 8192, where K is not a multiple of
+    1024, from K = 2048 over at most 4096 gate rows or from K = 3072 over at
+    most 8192; elsewhere the size is 0,
     so the Python layer allocates no workspace it never uses. A plan that does
     not split K needs none either."""
     lib = _backend.load()
     assert lib.ra_w8a16_gateup_workspace_size(16, 14336, 4096, 1) == 0     # the one-pass kernels
     assert lib.ra_w8a16_gateup_workspace_size(17, 28672, 8192, 1) == 0     # a one-split plan
     assert lib.ra_w8a16_gateup_workspace_size(32, 14336, 4096, 1) > _backend.WORKSPACE_COUNTER_BYTES
-    assert lib.ra_w8a16_gateup_workspace_size(8, 4097, 8192, 1) == 0
-    assert lib.ra_w8a16_gateup_workspace_size(16, 4097, 8192, 1) > _backend.WORKSPACE_COUNTER_BYTES
+    assert lib.ra_w8a16_gateup_workspace_size(8, 11008, 4096, 1) == 0
+    assert lib.ra_w8a16_gateup_workspace_size(8, 4096, 1024, 1) == 0
+    assert lib.ra_w8a16_gateup_workspace_size(8, 4097, 8192, 1) > _backend.WORKSPACE_COUNTER_BYTES
+    assert lib.ra_w8a16_gateup_workspace_size(8, 2048, 4096, 1) > _backend.WORKSPACE_COUNTER_BYTES
     assert lib.ra_w8a16_gateup_workspace_size(17, 3000, 16384, 1) > _backend.WORKSPACE_COUNTER_BYTES
     assert lib.ra_w8a16_gateup_workspace_size(1, 3000, 16384, 1) == 0      # the row GEMV
     assert lib.ra_w8a16_gateup_workspace_size(48, 3000, 4096, 1) > _backend.WORKSPACE_COUNTER_BYTES

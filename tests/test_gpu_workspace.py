@@ -115,12 +115,14 @@ def _check_chain(h, g64, u64, dt, gslack, uslack):
                                         (48, 4096, 3000), (33, 3584, 4200), (64, 8192, 2000), (2, 8192, 3584),
                                         (24, 12288, 1000),
                                         # M = 2..32: from 24 rows, from 16 rows at K = 8192, K not a
-                                        # multiple of 1024
-                                        (24, 4096, 6000), (16, 8192, 5000), (8, 4224, 3000)])
+                                        # multiple of 1024, M = 17, few gate rows from K = 2048
+                                        (24, 4096, 6000), (16, 8192, 5000), (8, 4224, 3000), (17, 2048, 3000),
+                                        (8, 2048, 2000), (4, 3072, 7000)])
 def test_gateup_splitk_vs_exact_and_oracle(gpu, dt, M, K, inter):
     """The gate/up + SwiGLU GEMM through the split-K kernel (K >= 16384, M =
-    33..64, at most 4096 gate rows from K = 8192, or M = 2..32 from 24 rows,
-    from 16 rows at K = 8192 or with K not a multiple of 1024; a workspace is asked for
+    33..64, at most 4096 gate rows from K = 8192, or M = 2..32 at M = 17,
+    from 24 rows, from 16 rows at K = 8192, with K not a multiple of 1024 or
+    over few gate rows from K = 2048; a workspace is asked for
     and given). Exact integer sums make the fp32 gate
     and up values order-independent, so the output must be the reference
     composition's roundings of them bit for bit (up to silu's own fp32
@@ -177,7 +179,7 @@ SPLITK_INSTANCES = [
     (False, 33, 11008, 3136, 8, 1, 8), (False, 33, 14336, 10304, 8, 2, 5), (False, 33, 8192, 40960, 8, 3, 2),
     (False, 16, 9088, 10944, 4, 3, 4), (False, 24, 2048, 29568, 4, 2, 1), (False, 33, 4096, 33344, 4, 3, 1),
     (False, 34, 4608, 64, 4, 1, 6), (False, 63, 6784, 3328, 8, 1, 8), (False, 48, 8832, 10496, 8, 2, 5),
-    (False, 38, 8192, 21888, 4, 3, 2),
+    (False, 38, 8192, 21888, 4, 3, 2), (False, 33, 512, 28672, 4, 2, 1),
     (True, 3, 8192, 128, 4, 1, 11), (True, 8, 16384, 3136, 8, 1, 8), (True, 3, 16384, 10816, 8, 2, 5),
     (True, 17, 16384, 128, 4, 1, 13), (True, 17, 16384, 3136, 8, 1, 8), (True, 17, 16384, 10304, 8, 2, 5),
     (True, 17, 8192, 128, 4, 1, 8), (True, 24, 16384, 3136, 8, 1, 8), (True, 18, 16384, 10304, 8, 2, 5),
