@@ -31,6 +31,7 @@ int g_sk_dmax = 0;
 int g_sk_x1 = 0;
 int g_sk_tw = 0;
 int g_sk_nw = 0;
+int g_sk_mt3 = 0;
 int g_tiled_split = 0;
 int g_w8a8_mode = 0;
 int g_gu_splitk = 0;
@@ -113,6 +114,12 @@ bool short_k_batch(const GemmArgs &a) {
 //    6144+ rows from K = 5120 (K=5120 N=6144 19.7 -> 15.5); the 64-row tiles
 //    and the small-batch kernel stay ahead below those (K=4096 N=8192 16.1
 //    against 17.5, K=2048 N=8192 9.9 against 11.3).
+//  * M = 34..48 (three 16-row tiles): over 28672+ rows (M=40 K=3072 N=57344
+//    +25 %, K=4096 N=28672 +23 %; level at K=1024 N=28672), from K = 4096
+//    over 6144+ rows (M=40 K=5120 N=11008 +19 %, K=4096 N=6144 +15 %; level
+//    at K=4096 N=8192-16384), at K = 3072 over at most 2048 rows (M=40 +9 %);
+//    the tiles and the small-batch kernel stay ahead at K <= 2048 below 28672
+//    rows (M=48 K=2048 N=11008 24 % behind) and at K = 3072 over 4096-16384.
 //  * M = 33..64 against the 64-row tiles: up to M = 48 from K = 8192 (M=33
 //    K=8192 N=8192 25.5 -> 22.7, N=16384 41.2 -> 33.0); over 32768+ rows
 //    from K = 4096 (M=40 K=4096 N=32768 39.6 -> 33.1, M=64 K=8192 66.5 ->
@@ -131,7 +138,14 @@ bool splitk_wanted(const GemmArgs &a) {
     if (a.K < 5120) return false;
     return a.N >= 14336 || a.K >= 11008 || (a.M >= 16 && a.K >= 8192) || a.M >= 24;
   }
-  if (a.M == 33 && (a.N >= 28672 || (a.K >= 4096 && a.N >= 11008) || (a.K >= 5120 && a.N >= 6144))) return true;
+  if (a.M <= 48) {
+    if (a.N >= 28672) return true;
+    if (a.M == 33) {
+      if ((a.K >= 4096 && a.N >= 11008) || (a.K >= 5120 && a.N >= 6144)) return true;
+    } else if ((a.K >= 4096 && a.N >= 6144) || (a.K >= 3072 && a.N <= 2048)) {
+      return true;
+    }
+  }
   if (a.N <= 4096) return a.K >= 4096;
   if (a.M <= 48 && a.K >= 8192) return true;
   if (a.N >= 32768) return a.K >= 4096;
@@ -170,11 +184,14 @@ bool splitk_selected(const GemmArgs &a, bool have_ws) {
 // one-pass kernels stay ahead, M=2 I=4096 6.8 against 7.9). At M = 17 the
 // extra-row form makes split K the faster at any K and I (K=4096 I=4096
 // 22.3 -> 12.8, K=4096 I=11008 23.7 -> 22.2, K=2048 I=28672 26.9 -> 22.6;
-// at most 4 % behind at K=2048-6144 I=11008).
+// at most 4 % behind at K=2048-6144 I=11008). At M = 33..47 over at most
+// 4096 gate rows from K = 6144, and from 40 rows at K = 4096 (M=40 K=6144
+// I=2048 21.9 -> 16.7, M=44 K=4096 I=2048 16.6 -> 15.4; M=36 K=4096 level,
+// K <= 3072 behind: M=40 K=2048 I=4096 10.8 against 13.3).
 bool gateup_splitk_wanted(int64_t M, int64_t I, int64_t K) {
   if (M < 2 || M > kSkinnyMaxM) return false;
   if (K >= kSplitkMinK || (K >= 8192 && I <= 4096)) return true;
-  if (M > 32) return I > 4096 || M >= 48;
+  if (M > 32) return I > 4096 || M >= 48 || K >= 6144 || (K >= 4096 && M >= 40);
   if (M == 17 || (K >= 2048 && I <= 4096) || (K >= 3072 && I <= 8192)) return true;
   return M >= 24 || (M >= 16 && K >= 8192) || K % 1024 != 0;
 }
@@ -269,6 +286,7 @@ void ra_tune_sk(int s, int dmax) { ra::g_sk_s = s; ra::g_sk_dmax = dmax; }
 void ra_tune_sk_x1(int off) { ra::g_sk_x1 = off; }
 void ra_tune_sk_tw(int tw) { ra::g_sk_tw = tw; }
 void ra_tune_sk_nw(int nw) { ra::g_sk_nw = nw; }
+void ra_tune_sk_mt3(int off) { ra::g_sk_mt3 = off; }
 void ra_tune_tiled_split(int v) { ra::g_tiled_split = v; }
 void ra_tune_w8a8(int mode) { ra::g_w8a8_mode = mode; }
 void ra_tune_rows_lds(int v) { ra::g_rows_lds = v; }

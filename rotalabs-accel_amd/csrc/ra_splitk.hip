@@ -43,7 +43,7 @@
 
 namespace ra {
 #ifdef RA_TUNING
-extern int g_sk_s, g_sk_dmax, g_sk_x1, g_sk_tw, g_sk_nw;  // tuning builds: forced split count, depth cap, extra-row form, tiles per wave, waves
+extern int g_sk_s, g_sk_dmax, g_sk_x1, g_sk_tw, g_sk_nw, g_sk_mt3;  // tuning builds: forced split count, depth cap, extra-row form, tiles per wave, waves, no 48-row tile
 #endif
 
 namespace sk {
@@ -70,8 +70,9 @@ constexpr int lds_bytes(int mt, int tw, bool gu, int d, int x1 = 0, int nw = NW)
 }
 // Activation copies per wave per stage and rows per copy: the stage's 16*MT
 // rows of 256 bytes are copied by the nw waves, 4 rows (64 lanes x 16 bytes)
-// per copy, or 2 rows (lanes 0..31) when 8 waves share 16 rows.
-constexpr int xcw(int mt, int nw) { return (4 * mt + nw - 1) / nw; }
+// per copy where the 4*MT copies divide evenly among the waves, else 2 rows
+// (lanes 0..31) per copy (8 waves sharing 16 or 48 rows).
+constexpr int xcw(int mt, int nw) { return (4 * mt) % nw == 0 ? 4 * mt / nw : 8 * mt / nw; }
 constexpr int rpc(int mt, int nw) { return 16 * mt / (nw * xcw(mt, nw)); }
 constexpr int copies(int mt, int tw, bool gu, int x1 = 0, int nw = NW) {  // per wave per stage
   return 2 * ntw(tw, gu) + xcw(mt, nw) + x1;
@@ -421,7 +422,13 @@ __global__ __launch_bounds__(64 * NWT, 1) void splitk_kernel(const char *__restr
 // ----------------------------------------------------------------------------
 namespace {
 
-int sk_mt(int64_t M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
+// 16-row MFMA tiles per activation block: M = 33..48 in three.
+int sk_mt(int64_t M) {
+#ifdef RA_TUNING
+  if (g_sk_mt3 && M > 32) return 4;  // tuning builds: pad M = 33..48 to four tiles
+#endif
+  return M <= 16 ? 1 : (M <= 32 ? 2 : (M <= 48 ? 3 : 4));
+}
 
 bool sk_shape_ok(int x_dt, const void *x, int64_t ldx, const int8_t *w, int64_t ldw, int64_t M, int64_t wrows,
                  int64_t K) {
@@ -447,7 +454,7 @@ bool sk_shape_ok(int x_dt, const void *x, int64_t ldx, const int8_t *w, int64_t 
 bool x1_wanted(int64_t M, int64_t K, bool gu) {
 #ifdef RA_TUNING
   if (g_sk_x1 == 1) return false;  // tuning builds: 1 turns the extra-row form off, 2 on at any K
-  if (g_sk_x1 == 2) return M == 17 || M == 33;
+  if (g_sk_x1 == 2) return M == 17 || M == 33 || M == 49;
 #endif
   return M == 33 || (M == 17 && (gu || K >= 16384));
 }
@@ -598,18 +605,22 @@ void splitk_dispatch(const SplitkPlan &p, const void *x, int64_t ldx, const int8
       return splitk_go<DT, MT_, TW_, GU, X1_, 8>(p, x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, ws, s);
   RA_SK8(1, 1, 0) RA_SK8(1, 2, 0) RA_SK8(1, 3, 0)
   RA_SK8(2, 1, 0) RA_SK8(2, 2, 0) RA_SK8(2, 3, 0)
+  RA_SK8(3, 1, 0) RA_SK8(3, 2, 0) RA_SK8(3, 3, 0)
   RA_SK8(4, 1, 0) RA_SK8(4, 2, 0) RA_SK8(4, 3, 0)
   RA_SK8(1, 1, 1) RA_SK8(1, 2, 1) RA_SK8(1, 3, 1)
   RA_SK8(2, 1, 1) RA_SK8(2, 2, 1) RA_SK8(2, 3, 1)
+  RA_SK8(3, 1, 1) RA_SK8(3, 2, 1) RA_SK8(3, 3, 1)
 #undef RA_SK8
 #define RA_SK(MT_, TW_, X1_)                                                                                     \
   if (p.mt == MT_ && p.tw == TW_ && p.x1 == X1_)                                                               \
     return splitk_go<DT, MT_, TW_, GU, X1_>(p, x, ldx, w, ldw, scale, bias, bias_dt, y, ldy, M, N, K, ws, s);
   RA_SK(1, 1, 0) RA_SK(1, 2, 0) RA_SK(1, 3, 0)
   RA_SK(2, 1, 0) RA_SK(2, 2, 0) RA_SK(2, 3, 0)
+  RA_SK(3, 1, 0) RA_SK(3, 2, 0) RA_SK(3, 3, 0)
   RA_SK(4, 1, 0) RA_SK(4, 2, 0) RA_SK(4, 3, 0)
   RA_SK(1, 1, 1) RA_SK(1, 2, 1) RA_SK(1, 3, 1)
   RA_SK(2, 1, 1) RA_SK(2, 2, 1) RA_SK(2, 3, 1)
+  RA_SK(3, 1, 1) RA_SK(3, 2, 1) RA_SK(3, 3, 1)
 #undef RA_SK
 }
 

@@ -80,7 +80,7 @@ def test_argument_checks_without_device_work():
     assert lib.ra_w8a16_gemm_noalloc(n, 0, 0, n, 0, n, n, 0, n, 0, 0, 4, 4, n) == 0
 
 
-@pytest.mark.parametrize("M,expect", [(1, 5), (2, 6), (3, 6), (4, 6), (5, 6), (16, 6), (32, 6), (33, 7), (34, 2), (64, 2), (65, 2),
+@pytest.mark.parametrize("M,expect", [(1, 5), (2, 6), (3, 6), (4, 6), (5, 6), (16, 6), (32, 6), (33, 7), (48, 7), (49, 2), (64, 2), (65, 2),
                                       (2048, 2)])
 def test_variant_selection(M, expect):
     assert _backend.load().ra_w8a16_gemm_select(M, 11008, 4096, 0) == expect
@@ -108,7 +108,7 @@ def test_variant_selection_fallbacks():
     (1, 11008, 4096, 5),
     # M = 33..56 at short K over at most ~12K rows: the small-batch kernel instead of the 64-row tiles
     (33, 8192, 2048, 6), (40, 12288, 3072, 6), (48, 11008, 1024, 6), (56, 8192, 2048, 6),
-    (48, 9216, 2048, 2), (33, 13824, 2048, 2), (64, 8192, 2048, 2), (40, 11008, 4096, 2),
+    (48, 9216, 2048, 2), (33, 13824, 2048, 2), (64, 8192, 2048, 2), (56, 11008, 4096, 2),
     # M = 17..32, K = 2048..4096 over 28672+ rows: the split-K kernel without a split (no workspace)
     (32, 28672, 4096, 7), (17, 28672, 4096, 7), (20, 40960, 2048, 7), (24, 24576, 4096, 6),
     (16, 28672, 4096, 6),
@@ -128,7 +128,11 @@ def test_variant_selection_fallbacks():
     # 64-row tiles
     (33, 16384, 16384, 7), (48, 8192, 28672, 7), (64, 32768, 16384, 7), (40, 32768, 8192, 7),
     (64, 4096, 8192, 7), (64, 16384, 16384, 7), (40, 16384, 8192, 7), (48, 32768, 4096, 7),
-    (64, 8192, 28672, 2), (48, 16384, 4096, 2), (64, 8192, 8192, 2), (56, 8192, 8192, 2)])
+    (64, 8192, 28672, 2), (56, 16384, 4096, 2), (64, 8192, 8192, 2), (56, 8192, 8192, 2),
+    # M = 34..48 (three 16-row tiles): over 28672+ rows, from K = 4096 over 6144+ rows, at
+    # K = 3072 over at most 2048 rows
+    (40, 28672, 1024, 7), (48, 16384, 4096, 7), (36, 6144, 4096, 7), (40, 2048, 3072, 7),
+    (40, 4096, 3072, 6), (48, 11008, 2048, 2)])
 def test_variant_selection_short_k_and_wide(M, N, K, expect):
     lib = _backend.load()
     assert lib.ra_w8a16_gemm_select(M, N, K, 1) == expect

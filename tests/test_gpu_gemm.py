@@ -184,7 +184,7 @@ def test_exact_known_answer_small_tile(gpu, M, K, N, dt):
 # (64 x 64*bnb tiles, nsplit splits; bnb/nsplit from the plan at 256 CUs):
 # 2/4, 2/3, 3/4, 3/2, 3/1, 2/2, 2/1, 1/2 -- K tiles not a multiple of the
 # split count, N tails, the partial sums of up to four splits combined.
-SPLIT_TILE_SHAPES = [(49, 9216, 8192), (64, 8192, 9000), (50, 6144, 12000), (64, 4096, 16500), (48, 1024, 40000),
+SPLIT_TILE_SHAPES = [(49, 9216, 8192), (64, 8192, 9000), (50, 6144, 12000), (64, 4096, 16500), (56, 1024, 40000),
                      (64, 6144, 16384), (40, 2048, 24000), (64, 6144, 8192),
                      # M = 65..128: two rows of 64-row tiles or one row of 128-row tiles (ragged M
                      # and N; 128 x 128 and 128 x 192 tiles with and without K splits)
@@ -385,13 +385,14 @@ def test_selection_rule_shapes_exact_and_oracle(gpu, M, K, N, dt):
 
 # Shapes the split-K selection rules send to the split-K kernel (M = 2..32 from
 # K = 5120 over 14336+ rows, at any M from K = 11008, from 16 rows at K = 8192,
-# from 24 rows, from 28 rows over at most 4096 rows from K = 3072; M = 33 over
-# many rows; M = 33..64 up to 48 rows from K = 8192, from K = 14336, over at
+# from 24 rows, from 28 rows over at most 4096 rows from K = 3072; M = 33..48
+# over many rows; M = 33..64 up to 48 rows from K = 8192, from K = 14336, over at
 # most 4096 rows from K = 4096; K >= 16384), with the plans the time model
 # picks there.
 SPLITK_RULE_SHAPES = [(2, 5120, 14400), (16, 11008, 6000), (24, 5120, 4000), (32, 5120, 6000), (40, 4096, 4000),
                       (48, 14336, 5000), (4, 16384, 4800), (64, 4096, 4096), (3, 11008, 2000), (16, 8192, 5000),
-                      (40, 8192, 9000), (30, 3072, 4000), (33, 1024, 30000), (33, 5120, 6200)]
+                      (40, 8192, 9000), (30, 3072, 4000), (33, 1024, 30000), (33, 5120, 6200), (40, 4096, 6200),
+                      (36, 3072, 2000)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
@@ -437,10 +438,11 @@ def test_splitk_selected_for_long_k():
     for M in (3, 16, 32):
         assert lib.ra_w8a16_gemm_select(M, 11008, 4096, _backend.F16) == BATCH
     # M = 33..64 with >= 8192 weight rows: the tiled kernel's 64 x 64 tile
-    for M in (34, 64):
+    for M in (49, 64):
         assert lib.ra_w8a16_gemm_select(M, 11008, 4096, _backend.F16) == TILED
-    # M = 33: one 16-row tile fewer and the extra row on the VALU, split K
-    assert lib.ra_w8a16_gemm_select(33, 11008, 4096, _backend.F16) == SPLITK
+    # M = 33..48: split K (three 16-row tiles, or two and the extra row on the VALU)
+    for M in (33, 40, 48):
+        assert lib.ra_w8a16_gemm_select(M, 11008, 4096, _backend.F16) == SPLITK
     # from 24 rows over at most 4096 weight rows: split K (M = 64 from K = 4096)
     assert lib.ra_w8a16_gemm_select(64, 4096, 4096, _backend.F16) == SPLITK
     assert lib.ra_w8a16_gemm_select(24, 4096, 4096, _backend.F16) == BATCH

@@ -117,10 +117,13 @@ def _check_chain(h, g64, u64, dt, gslack, uslack):
                                         # M = 2..32: from 24 rows, from 16 rows at K = 8192, K not a
                                         # multiple of 1024, M = 17, few gate rows from K = 2048
                                         (24, 4096, 6000), (16, 8192, 5000), (8, 4224, 3000), (17, 2048, 3000),
-                                        (8, 2048, 2000), (4, 3072, 7000)])
+                                        (8, 2048, 2000), (4, 3072, 7000),
+                                        # M = 33..47 over few gate rows from K = 6144, from 40 rows at 4096
+                                        (40, 6144, 2000), (44, 4096, 2000)])
 def test_gateup_splitk_vs_exact_and_oracle(gpu, dt, M, K, inter):
     """The gate/up + SwiGLU GEMM through the split-K kernel (K >= 16384, M =
-    33..64, at most 4096 gate rows from K = 8192, or M = 2..32 at M = 17,
+    33..64 (over few gate rows from K = 6144, or from 40 rows at K = 4096),
+    at most 4096 gate rows from K = 8192, or M = 2..32 at M = 17,
     from 24 rows, from 16 rows at K = 8192, with K not a multiple of 1024 or
     over few gate rows from K = 2048; a workspace is asked for
     and given). Exact integer sums make the fp32 gate
@@ -179,17 +182,19 @@ SPLITK_INSTANCES = [
     (False, 33, 11008, 3136, 8, 1, 8), (False, 33, 14336, 10304, 8, 2, 5), (False, 33, 8192, 40960, 8, 3, 2),
     (False, 16, 9088, 10944, 4, 3, 4), (False, 24, 2048, 29568, 4, 2, 1), (False, 33, 4096, 33344, 4, 3, 1),
     (False, 34, 4608, 64, 4, 1, 6), (False, 63, 6784, 3328, 8, 1, 8), (False, 48, 8832, 10496, 8, 2, 5),
-    (False, 38, 8192, 21888, 4, 3, 2), (False, 33, 512, 28672, 4, 2, 1),
-    (True, 3, 8192, 128, 4, 1, 11), (True, 8, 16384, 3136, 8, 1, 8), (True, 3, 16384, 10816, 8, 2, 5),
-    (True, 17, 16384, 128, 4, 1, 13), (True, 17, 16384, 3136, 8, 1, 8), (True, 17, 16384, 10304, 8, 2, 5),
-    (True, 17, 8192, 128, 4, 1, 8), (True, 24, 16384, 3136, 8, 1, 8), (True, 18, 16384, 10304, 8, 2, 5),
-    (True, 18, 16384, 40960, 4, 3, 1), (True, 33, 16384, 128, 4, 1, 10), (True, 33, 16384, 3136, 8, 1, 8),
-    (True, 33, 16384, 10304, 8, 2, 5), (True, 33, 16384, 11584, 4, 3, 4), (True, 48, 4096, 128, 4, 1, 4),
-    (True, 33, 4096, 8256, 8, 1, 3), (True, 33, 4096, 40960, 4, 3, 1),
-    (True, 3, 128, 16576, 4, 2, 1), (True, 13, 2304, 20928, 4, 3, 2), (True, 17, 128, 34688, 4, 3, 1),
-    (True, 17, 128, 17216, 4, 2, 1), (True, 23, 1536, 64, 4, 1, 4), (True, 28, 128, 16576, 4, 2, 1),
-    (True, 33, 128, 17856, 4, 2, 1), (True, 64, 3200, 8320, 8, 1, 3), (True, 40, 128, 17216, 4, 2, 1),
-    (True, 60, 128, 32896, 4, 3, 1)]
+    (False, 38, 8192, 21888, 4, 3, 2), (False, 33, 512, 28672, 4, 2, 1), (True, 3, 8192, 128, 4, 1, 11),
+    (True, 8, 16384, 3136, 8, 1, 8), (True, 3, 16384, 10816, 8, 2, 5), (True, 17, 16384, 128, 4, 1, 13),
+    (True, 17, 16384, 3136, 8, 1, 8), (True, 17, 16384, 10304, 8, 2, 5), (True, 17, 8192, 128, 4, 1, 8),
+    (True, 24, 16384, 3136, 8, 1, 8), (True, 18, 16384, 10304, 8, 2, 5), (True, 18, 16384, 40960, 4, 3, 1),
+    (True, 33, 16384, 128, 4, 1, 10), (True, 33, 16384, 3136, 8, 1, 8), (True, 33, 16384, 10304, 8, 2, 5),
+    (True, 33, 16384, 11584, 4, 3, 4), (True, 48, 4096, 128, 4, 1, 4), (True, 33, 4096, 8256, 8, 1, 3),
+    (True, 33, 4096, 40960, 4, 3, 1), (True, 3, 128, 16576, 4, 2, 1), (True, 13, 2304, 20928, 4, 3, 2),
+    (True, 17, 128, 34688, 4, 3, 1), (True, 17, 128, 17216, 4, 2, 1), (True, 23, 1536, 64, 4, 1, 4),
+    (True, 28, 128, 16576, 4, 2, 1), (True, 33, 128, 17856, 4, 2, 1), (True, 64, 3200, 8320, 8, 1, 3),
+    (True, 40, 128, 17216, 4, 2, 1), (True, 60, 128, 32896, 4, 3, 1), (False, 41, 7936, 3136, 8, 1, 8),
+    (False, 48, 4352, 33088, 8, 3, 2), (False, 53, 4480, 64, 4, 1, 7), (False, 59, 14336, 10432, 8, 2, 5),
+    (False, 60, 4096, 33088, 4, 3, 1), (True, 45, 2688, 8832, 8, 1, 3), (True, 45, 128, 32896, 4, 3, 1),
+    (True, 57, 1920, 64, 4, 1, 3), (True, 61, 128, 17088, 4, 2, 1), (False, 38, 128, 28672, 4, 2, 1)]
 
 
 class _SplitkPlan(ctypes.Structure):
