@@ -120,6 +120,18 @@ bool short_k_batch(const GemmArgs &a) {
 //    at K=4096 N=8192-16384), at K = 3072 over at most 2048 rows (M=40 +9 %);
 //    the tiles and the small-batch kernel stay ahead at K <= 2048 below 28672
 //    rows (M=48 K=2048 N=11008 24 % behind) and at K = 3072 over 4096-16384.
+//  * M = 49..64 (four 16-row tiles): below 8192 rows from K = 4096 and
+//    below 6144 from K = 3072, where the small-batch kernel runs (M=64
+//    K=8192 N=6144 35.4 -> 21.7, K=3584 N=4608 18.4 -> 15.6; M=52 K=3072
+//    N=6144 7.8 % behind); over 57344+ rows (M=52 K=1024 +23 %; at M=64 from
+//    K = 3072); over 28672-32768 rows from K = 2048 up to M = 56 (M=56 K=2048
+//    +6 %), from K = 4096 at M = 57..64 (M=64 K=11008 +12 %; over 37888
+//    rows the plan's 192-row units leave CUs idle: M=52 K=3584 39.7 against
+//    48.7 for the tiles); over 16384+ rows from
+//    K = 5120 (M=64 K=11008 N=16384 +7 %); up to M = 56 over 8192 rows from
+//    K = 8192 (M=52 K=11008 +10 %). The 64-row tiles stay ahead over
+//    8192-16384 rows at K <= 4096 (M=64 K=4096 N=11008 11 % behind) and over
+//    11008 rows at any K (M=56 K=8192 5 % behind).
 //  * M = 33..64 against the 64-row tiles: up to M = 48 from K = 8192 (M=33
 //    K=8192 N=8192 25.5 -> 22.7, N=16384 41.2 -> 33.0); over 32768+ rows
 //    from K = 4096 (M=40 K=4096 N=32768 39.6 -> 33.1, M=64 K=8192 66.5 ->
@@ -146,10 +158,17 @@ bool splitk_wanted(const GemmArgs &a) {
       return true;
     }
   }
+  if (a.M > 48) {
+    if (a.N < 8192) return a.K >= 4096 || (a.K >= 3072 && a.N < 6144);
+    if (a.N >= 57344) return a.M <= 56 || a.K >= 3072;
+    if (a.N >= 28672 && a.N <= 32768) return a.K >= (a.M <= 56 ? 2048 : 4096);
+    if (a.N >= 16384 && a.K >= 5120) return true;
+    if (a.M <= 56 && a.K >= 8192 && a.N <= 8192) return true;
+    return a.K >= 14336 && (a.N > 8192 || a.M <= 56);
+  }
   if (a.N <= 4096) return a.K >= 4096;
-  if (a.M <= 48 && a.K >= 8192) return true;
+  if (a.K >= 8192) return true;
   if (a.N >= 32768) return a.K >= 4096;
-  if (a.K >= 14336) return a.N > 8192 || a.M <= 56;
   return false;
 }
 

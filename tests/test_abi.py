@@ -128,11 +128,16 @@ def test_variant_selection_fallbacks():
     # 64-row tiles
     (33, 16384, 16384, 7), (48, 8192, 28672, 7), (64, 32768, 16384, 7), (40, 32768, 8192, 7),
     (64, 4096, 8192, 7), (64, 16384, 16384, 7), (40, 16384, 8192, 7), (48, 32768, 4096, 7),
-    (64, 8192, 28672, 2), (56, 16384, 4096, 2), (64, 8192, 8192, 2), (56, 8192, 8192, 2),
+    (64, 8192, 28672, 2), (56, 16384, 4096, 2), (64, 8192, 8192, 2), (56, 11008, 8192, 2),
     # M = 34..48 (three 16-row tiles): over 28672+ rows, from K = 4096 over 6144+ rows, at
     # K = 3072 over at most 2048 rows
     (40, 28672, 1024, 7), (48, 16384, 4096, 7), (36, 6144, 4096, 7), (40, 2048, 3072, 7),
-    (40, 4096, 3072, 6), (48, 11008, 2048, 2)])
+    (40, 4096, 3072, 6), (48, 11008, 2048, 2),
+    # M = 49..64 (four 16-row tiles): below 8192 rows from K = 4096 (below 6144 from K = 3072), over
+    # 57344+ rows (from K = 3072 at M > 56), over 28672-32768 from K = 2048 (4096 at M > 56), over
+    # 16384+ from K = 5120, up to M = 56 over 8192 rows from K = 8192
+    (64, 6144, 4096, 7), (52, 4608, 3584, 7), (52, 6144, 3072, 6), (52, 37888, 3584, 2), (52, 57344, 1024, 7), (64, 57344, 1024, 2), (56, 28672, 2048, 7), (64, 28672, 2048, 2),
+    (64, 16384, 5120, 7), (56, 8192, 8192, 7), (64, 11008, 4096, 2), (64, 16384, 4096, 2), (60, 6144, 2048, 6)])
 def test_variant_selection_short_k_and_wide(M, N, K, expect):
     lib = _backend.load()
     assert lib.ra_w8a16_gemm_select(M, N, K, 1) == expect

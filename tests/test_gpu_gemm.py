@@ -184,8 +184,8 @@ def test_exact_known_answer_small_tile(gpu, M, K, N, dt):
 # (64 x 64*bnb tiles, nsplit splits; bnb/nsplit from the plan at 256 CUs):
 # 2/4, 2/3, 3/4, 3/2, 3/1, 2/2, 2/1, 1/2 -- K tiles not a multiple of the
 # split count, N tails, the partial sums of up to four splits combined.
-SPLIT_TILE_SHAPES = [(49, 9216, 8192), (64, 8192, 9000), (50, 6144, 12000), (64, 4096, 16500), (56, 1024, 40000),
-                     (64, 6144, 16384), (40, 2048, 24000), (64, 6144, 8192),
+SPLIT_TILE_SHAPES = [(57, 9216, 8192), (64, 8192, 9000), (50, 6144, 12000), (64, 4096, 16500), (56, 1024, 40000),
+                     (60, 4096, 16384), (40, 2048, 24000), (64, 6144, 8192),
                      # M = 65..128: two rows of 64-row tiles or one row of 128-row tiles (ragged M
                      # and N; 128 x 128 and 128 x 192 tiles with and without K splits)
                      (65, 2048, 4096), (100, 11008, 4096), (128, 4096, 8200), (80, 6144, 9000), (97, 1024, 3000),
@@ -386,13 +386,14 @@ def test_selection_rule_shapes_exact_and_oracle(gpu, M, K, N, dt):
 # Shapes the split-K selection rules send to the split-K kernel (M = 2..32 from
 # K = 5120 over 14336+ rows, at any M from K = 11008, from 16 rows at K = 8192,
 # from 24 rows, from 28 rows over at most 4096 rows from K = 3072; M = 33..48
-# over many rows; M = 33..64 up to 48 rows from K = 8192, from K = 14336, over at
+# over many rows; M = 49..64 below 8192 rows from K = 3072 and over many rows;
+# M = 33..64 up to 48 rows from K = 8192, from K = 14336, over at
 # most 4096 rows from K = 4096; K >= 16384), with the plans the time model
 # picks there.
 SPLITK_RULE_SHAPES = [(2, 5120, 14400), (16, 11008, 6000), (24, 5120, 4000), (32, 5120, 6000), (40, 4096, 4000),
                       (48, 14336, 5000), (4, 16384, 4800), (64, 4096, 4096), (3, 11008, 2000), (16, 8192, 5000),
                       (40, 8192, 9000), (30, 3072, 4000), (33, 1024, 30000), (33, 5120, 6200), (40, 4096, 6200),
-                      (36, 3072, 2000)]
+                      (36, 3072, 2000), (60, 3072, 6000), (52, 2048, 30000)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])

@@ -193,8 +193,8 @@ SPLITK_INSTANCES = [
     (True, 28, 128, 16576, 4, 2, 1), (True, 33, 128, 17856, 4, 2, 1), (True, 64, 3200, 8320, 8, 1, 3),
     (True, 40, 128, 17216, 4, 2, 1), (True, 60, 128, 32896, 4, 3, 1), (False, 41, 7936, 3136, 8, 1, 8),
     (False, 48, 4352, 33088, 8, 3, 2), (False, 53, 4480, 64, 4, 1, 7), (False, 59, 14336, 10432, 8, 2, 5),
-    (False, 60, 4096, 33088, 4, 3, 1), (True, 45, 2688, 8832, 8, 1, 3), (True, 45, 128, 32896, 4, 3, 1),
-    (True, 57, 1920, 64, 4, 1, 3), (True, 61, 128, 17088, 4, 2, 1), (False, 38, 128, 28672, 4, 2, 1)]
+    (True, 45, 2688, 8832, 8, 1, 3), (True, 45, 128, 32896, 4, 3, 1), (True, 57, 1920, 64, 4, 1, 3),
+    (True, 61, 128, 17088, 4, 2, 1), (False, 38, 128, 28672, 4, 2, 1), (False, 64, 5120, 20928, 4, 3, 2)]
 
 
 class _SplitkPlan(ctypes.Structure):
