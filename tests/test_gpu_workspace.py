@@ -356,3 +356,43 @@ def test_workspace_call_runs_the_selected_kernel(gpu, M, N, K):
     assert torch.equal(y0, y1)
     ref = (x.float() @ q.float().T) * s
     torch.testing.assert_close(y0.float(), ref, rtol=1e-2, atol=1e-2)
+
+
+def _strided(gpu, t, ld):
+    """A (rows, cols) copy of t on the GPU with row stride ld elements."""
+    rows, cols = t.shape
+    store = torch.zeros((rows - 1) * ld + cols, dtype=t.dtype, device=gpu)
+    v = store.as_strided((rows, cols), (ld, 1))
+    v.copy_(t.to(gpu))
+    return v
+
+
+@pytest.mark.parametrize("gu,M,K,N", [(False, 17, 16384, 300), (False, 40, 4096, 4000), (False, 60, 3072, 6000),
+                                      (False, 5, 16384, 1000), (True, 33, 16384, 520), (True, 45, 4096, 2000),
+                                      (True, 17, 8192, 700)])
+def test_splitk_row_strides(gpu, gu, M, K, N):
+    """The split-K kernel with row strides on both operands (ldx = K + 8,
+    ldw = K + 48: every copy addresses its row through the stride) over the
+    tile forms (one, two with the extra row, three and four 16-row tiles;
+    GEMM and gate/up): bitwise the same output as contiguous operands (the
+    same plan, so the same order of sums)."""
+    dt = torch.bfloat16
+    g = torch.Generator().manual_seed(M + K + N)
+    rows = 2 * N if gu else N
+    x = torch.randn(M, K, generator=g).to(dt)
+    q = torch.randint(-127, 128, (rows, K), generator=g, dtype=torch.int8)
+    s = torch.rand(rows, generator=g) * 2e-3 + 1e-4
+    lib = _backend.load()
+    dcode = _backend.dtype_code(dt)
+    if gu:
+        assert lib.ra_w8a16_gateup_workspace_size(M, N, K, dcode) > _backend.WORKSPACE_COUNTER_BYTES
+    else:
+        assert lib.ra_w8a16_gemm_select(M, N, K, dcode) == _backend.VARIANT_SPLITK
+    print(f"  split-K strides gu={gu} M={M} K={K} N={N}", flush=True)
+    xs, qs, sd = _strided(gpu, x, K + 8), _strided(gpu, q, K + 48), s.to(gpu)
+    assert xs.stride(0) == K + 8 and qs.stride(0) == K + 48
+    fn = ra.int8_gateup_swiglu if gu else ra.int8_gemm
+    want = fn(x.to(gpu), q.to(gpu), sd)
+    got = fn(xs, qs, sd)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), f"max diff {(got.float() - want.float()).abs().max().item()}"
