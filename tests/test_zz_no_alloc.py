@@ -24,9 +24,10 @@ def test_noalloc_matches_workspace_entry_point(gpu):
     lib = _backend.load()
     stream = torch.cuda.current_stream(gpu).cuda_stream
     # (M, K, N, seed): the MLP's down projection at M=17, then a smaller split-K
-    # problem, then the 64-row tiles with K split over four workgroups, in one
-    # row and in two
-    for (M, K, N, seed) in [(17, 28672, 8192, 1), (5, 16384, 1000, 2), (64, 8192, 11008, 3), (128, 11008, 4096, 4)]:
+    # problem, split K with three 16-row tiles, then the 64-row tiles with K
+    # split over four workgroups, in one row and in two
+    for (M, K, N, seed) in [(17, 28672, 8192, 1), (5, 16384, 1000, 2), (40, 8192, 6000, 5), (64, 8192, 11008, 3),
+                            (128, 11008, 4096, 4)]:
         print(f"  noalloc M={M} K={K} N={N}", flush=True)
         c = gemm_case(M, K, N, seed, device=gpu, dtype=torch.bfloat16, outlier_rows=True)
         xdt = _backend.dtype_code(c.x.dtype)
