@@ -203,7 +203,11 @@ bool splitk_selected(const GemmArgs &a, bool have_ws) {
 // one-pass kernels stay ahead, M=2 I=4096 6.8 against 7.9). At M = 17 the
 // extra-row form makes split K the faster at any K and I (K=4096 I=4096
 // 22.3 -> 12.8, K=4096 I=11008 23.7 -> 22.2, K=2048 I=28672 26.9 -> 22.6;
-// at most 4 % behind at K=2048-6144 I=11008). At M = 33..47 over at most
+// at most 4 % behind at K=2048-6144 I=11008). At M = 18..23 (two 16-row
+// tiles either way) from K = 5120 (M=20 K=5120 I=11008 33.2 -> 29.6, I=28672
+// 59.2 -> 55.0) and at K <= 3072 over 14336+ gate rows (M=22 K=2048 I=28672
+// 27.3 -> 23.1); the one-pass kernels stay ahead at K <= 4096 over 11008
+// gate rows (M=18 K=2048 16.2 against 17.2). At M = 33..47 over at most
 // 4096 gate rows from K = 6144, and from 40 rows at K = 4096 (M=40 K=6144
 // I=2048 21.9 -> 16.7, M=44 K=4096 I=2048 16.6 -> 15.4; M=36 K=4096 level,
 // K <= 3072 behind: M=40 K=2048 I=4096 10.8 against 13.3).
@@ -212,6 +216,7 @@ bool gateup_splitk_wanted(int64_t M, int64_t I, int64_t K) {
   if (K >= kSplitkMinK || (K >= 8192 && I <= 4096)) return true;
   if (M > 32) return I > 4096 || M >= 48 || K >= 6144 || (K >= 4096 && M >= 40);
   if (M == 17 || (K >= 2048 && I <= 4096) || (K >= 3072 && I <= 8192)) return true;
+  if (M >= 18 && (K >= 5120 || (K <= 3072 && I >= 14336))) return true;
   return M >= 24 || (M >= 16 && K >= 8192) || K % 1024 != 0;
 }
 

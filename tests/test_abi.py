@@ -239,7 +239,8 @@ def test_gateup_workspace_only_where_gateup_splits():
     over at most 4096 gate rows, at M = 33..64, and at M = 2..32 at M = 17,
     from 24 rows, from 16 rows at K = 8192, where K is not a multiple of
     1024, from K = 2048 over at most 4096 gate rows or from K = 3072 over at
-    most 8192; elsewhere the size is 0,
+    most 8192, and from 18 rows at K >= 5120 or over 14336+ gate rows at
+    K <= 3072; elsewhere the size is 0,
     so the Python layer allocates no workspace it never uses. A plan that does
     not split K needs none either."""
     lib = _backend.load()
@@ -250,6 +251,8 @@ def test_gateup_workspace_only_where_gateup_splits():
     assert lib.ra_w8a16_gateup_workspace_size(8, 4096, 1024, 1) == 0
     assert lib.ra_w8a16_gateup_workspace_size(8, 4097, 8192, 1) > _backend.WORKSPACE_COUNTER_BYTES
     assert lib.ra_w8a16_gateup_workspace_size(8, 2048, 4096, 1) > _backend.WORKSPACE_COUNTER_BYTES
+    assert lib.ra_w8a16_gateup_workspace_size(20, 11008, 5120, 1) > _backend.WORKSPACE_COUNTER_BYTES
+    assert lib.ra_w8a16_gateup_workspace_size(18, 11008, 4096, 1) == 0
     assert lib.ra_w8a16_gateup_workspace_size(17, 3000, 16384, 1) > _backend.WORKSPACE_COUNTER_BYTES
     assert lib.ra_w8a16_gateup_workspace_size(1, 3000, 16384, 1) == 0      # the row GEMV
     assert lib.ra_w8a16_gateup_workspace_size(48, 3000, 4096, 1) > _backend.WORKSPACE_COUNTER_BYTES

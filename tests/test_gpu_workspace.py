@@ -119,13 +119,15 @@ def _check_chain(h, g64, u64, dt, gslack, uslack):
                                         (24, 4096, 6000), (16, 8192, 5000), (8, 4224, 3000), (17, 2048, 3000),
                                         (8, 2048, 2000), (4, 3072, 7000),
                                         # M = 33..47 over few gate rows from K = 6144, from 40 rows at 4096
-                                        (40, 6144, 2000), (44, 4096, 2000)])
+                                        (40, 6144, 2000), (44, 4096, 2000),
+                                        # M = 18..23 from K = 5120
+                                        (20, 5120, 3000), (21, 5120, 6000)])
 def test_gateup_splitk_vs_exact_and_oracle(gpu, dt, M, K, inter):
     """The gate/up + SwiGLU GEMM through the split-K kernel (K >= 16384, M =
     33..64 (over few gate rows from K = 6144, or from 40 rows at K = 4096),
     at most 4096 gate rows from K = 8192, or M = 2..32 at M = 17,
     from 24 rows, from 16 rows at K = 8192, with K not a multiple of 1024 or
-    over few gate rows from K = 2048; a workspace is asked for
+    over few gate rows from K = 2048, or from 18 rows at K >= 5120; a workspace is asked for
     and given). Exact integer sums make the fp32 gate
     and up values order-independent, so the output must be the reference
     composition's roundings of them bit for bit (up to silu's own fp32
