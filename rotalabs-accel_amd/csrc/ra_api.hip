@@ -107,7 +107,10 @@ bool short_k_batch(const GemmArgs &a) {
 //    against 15.8, M=16 K=5120 N=8192 12.4 against 13.5), except from 28
 //    rows at K = 3072..4096 over at most 4096 rows, where it has too few
 //    workgroups (M=32 K=4096 N=2048 11.2 -> 9.6, K=3072 N=1024 9.6 -> 8.9;
-//    M=24 K=3072 level, K=4096 N=4096 10.0 against 10.5).
+//    M=24 K=3072 level, K=4096 N=4096 10.0 against 10.5), and from 20 rows
+//    at K = 4096 over 14336-20480 rows, between the small-batch kernel's
+//    even rounds at 12288 and 24576 rows (M=32 N=14336 +29 %, M=24 N=16384
+//    +12 %, M=20 N=14336 +10 %; N=12288 7-15 % behind).
 //  * M = 33 (one 16-row tile fewer, the extra row on the VALU): over 28672+
 //    rows (M=33 K=3072 N=28672 28.1 -> 21.4, K=1024 N=57344 28.7 -> 19.3),
 //    over 11008+ rows from K = 4096 (K=4096 N=11008 20.4 -> 18.4), over
@@ -147,6 +150,7 @@ bool splitk_wanted(const GemmArgs &a) {
   if (a.M <= 32) {
     if (a.K >= kSplitkMinK) return true;
     if (a.M >= 28 && a.K >= 3072 && a.N <= 4096) return true;
+    if (a.M >= 20 && a.K == 4096 && a.N >= 14336 && a.N <= 20480) return true;
     if (a.K < 5120) return false;
     return a.N >= 14336 || a.K >= 11008 || (a.M >= 16 && a.K >= 8192) || a.M >= 24;
   }

@@ -117,8 +117,10 @@ def test_variant_selection_fallbacks():
     (32, 27648, 5120, 7), (2, 28672, 5120, 7), (8, 14336, 8192, 7), (16, 8192, 11008, 7),
     (24, 4096, 8192, 7), (32, 8192, 5120, 7), (24, 8192, 5120, 7), (2, 4096, 14336, 7), (16, 4096, 8192, 7),
     (8, 8192, 8192, 6), (16, 8192, 5120, 6), (4, 4096, 8192, 6),
-    # ... and from 28 rows at K = 3072..4096 over at most 4096 rows
+    # ... and from 28 rows at K = 3072..4096 over at most 4096 rows, from 20 rows at K = 4096 over
+    # 14336-20480 rows
     (32, 2048, 4096, 7), (28, 4096, 3072, 7), (24, 2048, 4096, 6), (32, 6144, 4096, 6), (32, 4096, 2048, 6),
+    (20, 14336, 4096, 7), (32, 20480, 4096, 7), (19, 14336, 4096, 6), (24, 12288, 4096, 6), (24, 24576, 4096, 6),
     # M = 33 (the extra-row form): over 28672+ rows, over 11008+ from K = 4096, over 6144+ from
     # K = 5120; the tiles or the small-batch kernel below
     (33, 28672, 3072, 7), (33, 57344, 1024, 7), (33, 11008, 4096, 7), (33, 6144, 5120, 7),

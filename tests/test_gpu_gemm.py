@@ -393,7 +393,7 @@ def test_selection_rule_shapes_exact_and_oracle(gpu, M, K, N, dt):
 SPLITK_RULE_SHAPES = [(2, 5120, 14400), (16, 11008, 6000), (24, 5120, 4000), (32, 5120, 6000), (40, 4096, 4000),
                       (48, 14336, 5000), (4, 16384, 4800), (64, 4096, 4096), (3, 11008, 2000), (16, 8192, 5000),
                       (40, 8192, 9000), (30, 3072, 4000), (33, 1024, 30000), (33, 5120, 6200), (40, 4096, 6200),
-                      (36, 3072, 2000), (60, 3072, 6000), (52, 2048, 30000)]
+                      (36, 3072, 2000), (60, 3072, 6000), (52, 2048, 30000), (24, 4096, 16000)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
