@@ -110,7 +110,9 @@ bool short_k_batch(const GemmArgs &a) {
 //    M=24 K=3072 level, K=4096 N=4096 10.0 against 10.5), and from 20 rows
 //    at K = 4096 over 14336-20480 rows, between the small-batch kernel's
 //    even rounds at 12288 and 24576 rows (M=32 N=14336 +29 %, M=24 N=16384
-//    +12 %, M=20 N=14336 +10 %; N=12288 7-15 % behind).
+//    +12 %, M=20 N=14336 +10 %; N=12288 7-15 % behind), and from K = 8192
+//    over at most 2048 rows, where the small-batch kernel has too few
+//    workgroups (M=8 K=8192 N=512 9.9 -> 8.1, N=2048 10.2 -> 9.0).
 //  * M = 33 (one 16-row tile fewer, the extra row on the VALU): over 28672+
 //    rows (M=33 K=3072 N=28672 28.1 -> 21.4, K=1024 N=57344 28.7 -> 19.3),
 //    over 11008+ rows from K = 4096 (K=4096 N=11008 20.4 -> 18.4), over
@@ -151,6 +153,7 @@ bool splitk_wanted(const GemmArgs &a) {
     if (a.K >= kSplitkMinK) return true;
     if (a.M >= 28 && a.K >= 3072 && a.N <= 4096) return true;
     if (a.M >= 20 && a.K == 4096 && a.N >= 14336 && a.N <= 20480) return true;
+    if (a.K >= 8192 && a.N <= 2048) return true;
     if (a.K < 5120) return false;
     return a.N >= 14336 || a.K >= 11008 || (a.M >= 16 && a.K >= 8192) || a.M >= 24;
   }
@@ -230,9 +233,15 @@ int select_variant(const GemmArgs &a, bool have_ws) {
   // streams each weight row once per activation row pair no faster than
   // the MFMA kernels (same run: K=4096 N=11008 9.6 vs 11.3 us, K=28672
   // N=8192 40.3 split K / 38.9 small batch vs 50.0, K=16384 N=16384 44.4 /
-  // 47.4 vs 56.2, K=8192 N=57344 81.1 small batch vs 95.0). M = 1 stays with
-  // the row GEMV (8.5 vs 9.8 at K=4096 N=11008, 37.3 vs 39.0 at K=28672).
-  if (gemv_rows_supported(a) && (a.M == 1 || !batch_supported(a))) {
+  // 47.4 vs 56.2, K=8192 N=57344 81.1 small batch vs 95.0), except over few
+  // rows, where the MFMA kernels' 16-row units leave most CUs idle: up to
+  // 1024 rows, and 2048 at K = 8192..16384 (K=8192 N=512 8.8 -> 4.2, N=2048
+  // 9.1 -> 6.9, K=28672 N=1024 13.2 -> 9.4 against split K, K=4096 N=1024
+  // 4.4 -> 3.9; K=28672 N=2048 12 % behind). M = 1 stays with the row GEMV
+  // (8.5 vs 9.8 at K=4096 N=11008, 37.3 vs 39.0 at K=28672).
+  const bool two_rows_few =
+      a.M == 2 && (a.N <= 1024 || (a.N <= 2048 && a.K >= 8192 && a.K <= 16384));
+  if (gemv_rows_supported(a) && (a.M == 1 || two_rows_few || !batch_supported(a))) {
     const int v = one_row_short_k(a);
     return v ? v : RA_VARIANT_ROWS;
   }

@@ -106,6 +106,8 @@ def test_variant_selection_fallbacks():
     # M = 1, K <= 2048 over 4096+ rows: the small-batch kernel (skinny at K <= 1536 over 16384+ rows)
     (1, 16384, 2048, 6), (1, 4096, 512, 6), (1, 16384, 1024, 1), (1, 2048, 1024, 5), (1, 16384, 3072, 5),
     (1, 11008, 4096, 5),
+    # M = 2 over few rows: the row GEMV (up to 1024 rows, 2048 at K = 8192..16384)
+    (2, 512, 8192, 5), (2, 1024, 4096, 5), (2, 2048, 16384, 5), (2, 2048, 28672, 7), (2, 2048, 4096, 6),
     # M = 33..56 at short K over at most ~12K rows: the small-batch kernel instead of the 64-row tiles
     (33, 8192, 2048, 6), (40, 12288, 3072, 6), (48, 11008, 1024, 6), (56, 8192, 2048, 6),
     (48, 9216, 2048, 2), (33, 13824, 2048, 2), (64, 8192, 2048, 2), (56, 11008, 4096, 2),
@@ -121,6 +123,8 @@ def test_variant_selection_fallbacks():
     # 14336-20480 rows
     (32, 2048, 4096, 7), (28, 4096, 3072, 7), (24, 2048, 4096, 6), (32, 6144, 4096, 6), (32, 4096, 2048, 6),
     (20, 14336, 4096, 7), (32, 20480, 4096, 7), (19, 14336, 4096, 6), (24, 12288, 4096, 6), (24, 24576, 4096, 6),
+    # ... and from K = 8192 over at most 2048 rows
+    (4, 512, 8192, 7), (8, 2048, 8192, 7), (8, 2048, 4096, 6),
     # M = 33 (the extra-row form): over 28672+ rows, over 11008+ from K = 4096, over 6144+ from
     # K = 5120; the tiles or the small-batch kernel below
     (33, 28672, 3072, 7), (33, 57344, 1024, 7), (33, 11008, 4096, 7), (33, 6144, 5120, 7),

@@ -393,7 +393,8 @@ def test_selection_rule_shapes_exact_and_oracle(gpu, M, K, N, dt):
 SPLITK_RULE_SHAPES = [(2, 5120, 14400), (16, 11008, 6000), (24, 5120, 4000), (32, 5120, 6000), (40, 4096, 4000),
                       (48, 14336, 5000), (4, 16384, 4800), (64, 4096, 4096), (3, 11008, 2000), (16, 8192, 5000),
                       (40, 8192, 9000), (30, 3072, 4000), (33, 1024, 30000), (33, 5120, 6200), (40, 4096, 6200),
-                      (36, 3072, 2000), (60, 3072, 6000), (52, 2048, 30000), (24, 4096, 16000)]
+                      (36, 3072, 2000), (60, 3072, 6000), (52, 2048, 30000), (24, 4096, 16000),
+                      (6, 8192, 1500)]
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
@@ -452,7 +453,7 @@ def test_splitk_selected_for_long_k():
 def test_two_rows_take_the_small_batch_kernels():
     """M = 2 runs the small-batch kernels wherever they apply (K % 128 == 0;
     split K from K = 11008, with a workspace from K = 16384), the row GEMV
-    only where they do not; M = 1 the row GEMV."""
+    where they do not and over few weight rows; M = 1 the row GEMV."""
     lib = _backend.load()
     assert lib.ra_w8a16_gemm_select(2, 11008, 4096, _backend.F16) == BATCH
     assert lib.ra_w8a16_gemm_select(2, 4096, 2048, _backend.BF16) == BATCH
@@ -461,6 +462,7 @@ def test_two_rows_take_the_small_batch_kernels():
     assert lib.ra_w8a16_gemm_select(2, 4096, 1024, _backend.F16) == BATCH
     assert lib.ra_w8a16_gemm_select(2, 8192, 28672, _backend.BF16) == SPLITK
     assert lib.ra_w8a16_gemm_select(2, 4096, 1040, _backend.F16) == ROWS
+    assert lib.ra_w8a16_gemm_select(2, 1024, 8192, _backend.F16) == ROWS   # few rows
     assert lib.ra_w8a16_gemm_select(1, 11008, 4096, _backend.F16) == ROWS
     assert lib.ra_w8a16_gemm_select(1, 8192, 28672, _backend.F16) == ROWS
     assert lib.ra_w8a16_gemm_workspace_size(2, 8192, 28672, _backend.BF16) > 0
