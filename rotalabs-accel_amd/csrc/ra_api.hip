@@ -35,6 +35,7 @@ int g_sk_mt3 = 0;
 int g_tiled_split = 0;
 int g_w8a8_mode = 0;
 int g_gu_splitk = 0;
+int g_gu_rows = 0;
 int g_rows_lds = 0;
 }
 #endif
@@ -227,6 +228,14 @@ bool gateup_splitk_wanted(int64_t M, int64_t I, int64_t K) {
   return M >= 24 || (M >= 16 && K >= 8192) || K % 1024 != 0;
 }
 
+// The gate/up product at M = 2 over few gate rows runs the row GEMV (same
+// run, bf16, us, previous pick -> row GEMV: K=4096 I=1024 9.4 -> 4.7,
+// I=4096 11.6 -> 9.6, K=8192 I=8192 29.5 -> 26.8, K=16384 I=1024 14.6 ->
+// 9.5; behind from I = 3584 at K = 16384 and at I = 14336).
+bool gateup_two_rows_few(int64_t M, int64_t I, int64_t K) {
+  return M == 2 && K % 16 == 0 && (I <= 2048 || (I <= 8192 && K <= 8192));
+}
+
 int select_variant(const GemmArgs &a, bool have_ws) {
   if (a.K == 0) return RA_VARIANT_GENERIC;
   // M = 2 runs the small-batch kernels where they apply: the row GEMV
@@ -328,6 +337,7 @@ void ra_tune_tiled_split(int v) { ra::g_tiled_split = v; }
 void ra_tune_w8a8(int mode) { ra::g_w8a8_mode = mode; }
 void ra_tune_rows_lds(int v) { ra::g_rows_lds = v; }
 void ra_tune_gu_splitk(int v) { ra::g_gu_splitk = v; }
+void ra_tune_gu_rows(int v) { ra::g_gu_rows = v; }
 #endif
 #ifdef RA_TRACE
 // Trace builds only: device buffer for the tiled kernel's per-workgroup timestamps (NULL: none).
@@ -431,7 +441,7 @@ int ra_w8a16_gemm_select(int64_t M, int64_t N, int64_t K, int x_dtype) {
 size_t ra_w8a16_gateup_workspace_size(int64_t M, int64_t I, int64_t K, int x_dtype) {
   if (x_dtype != RA_F16 && x_dtype != RA_BF16) return 0;
   // Only the split-K gate/up kernel uses a workspace, where it is selected.
-  if (!gateup_splitk_wanted(M, I, K) || K < 128 || K % 128 != 0) return 0;
+  if (!gateup_splitk_wanted(M, I, K) || gateup_two_rows_few(M, I, K) || K < 128 || K % 128 != 0) return 0;
   const SplitkPlan p = splitk_plan(M, I, K, true, true);
   return p.ok ? p.ws_bytes : 0;
 }
@@ -454,8 +464,11 @@ int ra_w8a16_gateup_swiglu_ws(const void *x, int64_t ldx, int x_dtype, const int
   const GateUpArgs a{x, ldx, x_dtype, w, ldw, scale, h, ldh, M, I, K};
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool have_ws = workspace != nullptr && workspace_bytes > 0;
-  if (K > 0 && gateup_gemv_rows_supported(a) && (M == 1 || !gateup_batch_supported(a)))
-    return to_status(gateup_gemv_rows_launch(a, s));
+  bool gu_rows = M == 1 || !gateup_batch_supported(a) || gateup_two_rows_few(M, I, K);
+#ifdef RA_TUNING
+  if (g_gu_rows) gu_rows = true;  // tuning builds: the row GEMV wherever it applies
+#endif
+  if (K > 0 && gateup_gemv_rows_supported(a) && gu_rows) return to_status(gateup_gemv_rows_launch(a, s));
   bool gu_split = gateup_splitk_wanted(M, I, K);
 #ifdef RA_TUNING
   if (g_gu_splitk) gu_split = g_gu_splitk > 0;  // tuning builds: 1 forces, -1 forbids the split-K kernel

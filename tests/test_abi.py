@@ -262,6 +262,7 @@ def test_gateup_workspace_only_where_gateup_splits():
     assert lib.ra_w8a16_gateup_workspace_size(17, 3000, 16384, 1) > _backend.WORKSPACE_COUNTER_BYTES
     assert lib.ra_w8a16_gateup_workspace_size(1, 3000, 16384, 1) == 0      # the row GEMV
     assert lib.ra_w8a16_gateup_workspace_size(48, 3000, 4096, 1) > _backend.WORKSPACE_COUNTER_BYTES
-    assert lib.ra_w8a16_gateup_workspace_size(2, 3584, 8192, 1) > _backend.WORKSPACE_COUNTER_BYTES
+    assert lib.ra_w8a16_gateup_workspace_size(2, 3584, 16384, 1) > _backend.WORKSPACE_COUNTER_BYTES
+    assert lib.ra_w8a16_gateup_workspace_size(2, 3584, 8192, 1) == 0   # M = 2, few gate rows: row GEMV
     assert lib.ra_w8a16_gateup_workspace_size(40, 3000, 4160, 1) == 0      # K % 128 != 0
 

@@ -255,13 +255,14 @@ def _swiglu_chain64(g64, u64, dt):
 # (17, 2048, 640): the gate/up kernel with the activation rows in LDS, one
 # or two 16-row activation tiles, in 8, 6, 1, 1, 8, 9 and 2 K chunks (1024,
 # 1024, 1536, 512, 1024, 512 and 1024 k), I not a multiple of 16;
-# (2, 8192, 3000): two rows in the same kernel (4 chunks of 2048 k);
+# (2, 8192, 9000): two rows in the same kernel (4 chunks of 2048 k);
+# (2, 8192, 3000): two rows over few gate rows, the row GEMV;
 # (16, 1024, 16448): more workgroups (257) than CUs, 512-k chunks;
 # (20, 256, 8192): the small-batch kernel with two activation tiles.
 @pytest.mark.parametrize("M,K,inter", [(1, 1024, 512), (5, 512, 300), (17, 2048, 640), (64, 256, 128),
                                         (5, 512, 8192), (20, 256, 8192), (1, 4096, 6000),
                                         (16, 8192, 3000), (13, 6144, 1000), (9, 1536, 777),
-                                        (17, 8192, 3000), (32, 4608, 1000), (2, 8192, 3000), (16, 1024, 16448),
+                                        (17, 8192, 3000), (32, 4608, 1000), (2, 8192, 3000), (2, 8192, 9000), (16, 1024, 16448),
                                         (100, 512, 96), (300, 1024, 200), (320, 128, 8704), (450, 128, 11264)])
 def test_gateup_swiglu_vs_oracle(gpu, dt, M, K, inter):
     g = torch.Generator().manual_seed(M + K)

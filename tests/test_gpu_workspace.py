@@ -108,11 +108,11 @@ def _check_chain(h, g64, u64, dt, gslack, uslack):
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("M,K,inter", [(17, 16384, 3000), (2, 16384, 700), (64, 32768, 1000), (5, 16384, 48),
+@pytest.mark.parametrize("M,K,inter", [(17, 16384, 3000), (3, 16384, 700), (64, 32768, 1000), (5, 16384, 48),
                                         (33, 16384, 520),
                                         # below K = 16384: M = 33..64 (from 48 rows or over 4096+ gate rows),
                                         # and at most 4096 gate rows from K = 8192
-                                        (48, 4096, 3000), (33, 3584, 4200), (64, 8192, 2000), (2, 8192, 3584),
+                                        (48, 4096, 3000), (33, 3584, 4200), (64, 8192, 2000), (2, 16384, 3584),
                                         (24, 12288, 1000),
                                         # M = 2..32: from 24 rows, from 16 rows at K = 8192, K not a
                                         # multiple of 1024, M = 17, few gate rows from K = 2048
