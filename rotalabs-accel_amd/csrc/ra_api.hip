@@ -158,14 +158,6 @@ bool splitk_wanted(const GemmArgs &a) {
     if (a.K < 5120) return false;
     return a.N >= 14336 || a.K >= 11008 || (a.M >= 16 && a.K >= 8192) || a.M >= 24;
   }
-  if (a.M <= 48) {
-    if (a.N >= 28672) return true;
-    if (a.M == 33) {
-      if ((a.K >= 4096 && a.N >= 11008) || (a.K >= 5120 && a.N >= 6144)) return true;
-    } else if ((a.K >= 4096 && a.N >= 6144) || (a.K >= 3072 && a.N <= 2048)) {
-      return true;
-    }
-  }
   if (a.M > 48) {
     if (a.N < 8192) return a.K >= 4096 || (a.K >= 3072 && a.N < 6144);
     if (a.N >= 57344) return a.M <= 56 || a.K >= 3072;
@@ -173,6 +165,13 @@ bool splitk_wanted(const GemmArgs &a) {
     if (a.N >= 16384 && a.K >= 5120) return true;
     if (a.M <= 56 && a.K >= 8192 && a.N <= 8192) return true;
     return a.K >= 14336 && (a.N > 8192 || a.M <= 56);
+  }
+  // M = 33..48
+  if (a.N >= 28672) return true;
+  if (a.M == 33) {
+    if ((a.K >= 4096 && a.N >= 11008) || (a.K >= 5120 && a.N >= 6144)) return true;
+  } else if ((a.K >= 4096 && a.N >= 6144) || (a.K >= 3072 && a.N <= 2048)) {
+    return true;
   }
   if (a.N <= 4096) return a.K >= 4096;
   if (a.K >= 8192) return true;
