@@ -138,16 +138,14 @@ bool short_k_batch(const GemmArgs &a) {
 //    K = 8192 (M=52 K=11008 +10 %). The 64-row tiles stay ahead over
 //    8192-16384 rows at K <= 4096 (M=64 K=4096 N=11008 11 % behind) and over
 //    11008 rows at any K (M=56 K=8192 5 % behind).
-//  * M = 33..64 against the 64-row tiles: up to M = 48 from K = 8192 (M=33
-//    K=8192 N=8192 25.5 -> 22.7, N=16384 41.2 -> 33.0); over 32768+ rows
-//    from K = 4096 (M=40 K=4096 N=32768 39.6 -> 33.1, M=64 K=8192 66.5 ->
-//    62.5); from K = 14336 except M > 56 over at most 8192 rows, where the
-//    two are level (M=64 K=16384 N=16384 67.9 -> 63.9; M=64 K=16384 N=8192
-//    38.8 against 39.9); at most 4096 rows from K = 4096, against the
-//    small-batch kernel (M=64 K=8192 N=4096 32.8 -> 19.8, M=64 K=4096 N=4096
-//    18.4 -> 14.8). The tiles stay ahead at K = 4096 over 8192-16384 rows
-//    (M=64 N=8192 15.1 against 18.7) and at M=64 K=8192 N=8192 (23.7 against
-//    24.4).
+//    With a long K: from K = 14336 except M > 56 over at most 8192 rows,
+//    where the two are level (M=64 K=16384 N=16384 67.9 -> 63.9; M=64
+//    K=16384 N=8192 38.8 against 39.9).
+//  * M = 33..48, beside the rules above: from K = 8192 (M=33 K=8192 N=8192
+//    25.5 -> 22.7, N=16384 41.2 -> 33.0); over 32768+ rows from K = 4096
+//    (M=40 K=4096 N=32768 39.6 -> 33.1); at most 4096 rows from K = 4096,
+//    against the small-batch kernel (M=64 K=8192 N=4096 32.8 -> 19.8, M=64
+//    K=4096 N=4096 18.4 -> 14.8, the same at M = 33..48).
 bool splitk_wanted(const GemmArgs &a) {
   if (a.M < 2 || a.M > kSkinnyMaxM) return false;
   if (a.M <= 32) {
